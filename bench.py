@@ -1,0 +1,587 @@
+"""Benchmark of the fused memory-bound kernels on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|adamw|copy]
+
+Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
+(8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
+``--layers`` independent activations (as the norms of consecutive decoder layers) and then
+their backward in reverse order, so no input is cache-resident when it is read (each
+activation is 134 MB; the working set of a step is ``layers`` x 537 MB against a 256 MB
+Infinity Cache).  Inputs are synthetic (seeded N(0,1), weight 1 + 0.02 N(0,1)) and
+resident in HBM before timing.
+
+Prints ONE JSON line: value = algorithmic bytes of the step / wall time of the step
+(decimal GB/s), with a ``roofline`` object for the dominant kernel (HIP events around each
+of its launches inside the timed region) and a ``cpu_baseline`` object (the reference's
+PyTorch fallback, restated in ``oracle/``, timed on this host's cores on a bounded sample
+of the same inputs).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from picotron_amd import _lib, ops  # noqa: E402
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E, 8 TB/s
+HEADLINE_METRIC = "RMSNorm/SwiGLU fwd+bwd HBM GB/s & % of peak, 16k tok×4096 bf16"
+
+
+def _seeded(shape, dtype, seed, scale=1.0, shift=0.0, device="cuda"):
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = torch.empty(shape, dtype=dtype, device=device)
+    # generate in fp32 slices to bound the temporary
+    flat = out.view(-1)
+    step = 1 << 28
+    for lo in range(0, flat.numel(), step):
+        hi = min(flat.numel(), lo + step)
+        flat[lo:hi] = (torch.randn(hi - lo, generator=g, device=device) * scale + shift).to(dtype)
+    return out
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _cpu_info() -> tuple[int, int, str]:
+    cores = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return cores, os.cpu_count() or cores, model
+
+
+def _time_cpu(fn, target_s: float = 2.0) -> float:
+    """Median of 3 timed calls after one warm-up (seconds per call)."""
+
+    fn()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+# ------------------------------------------------------------------ workloads
+
+
+class Workload:
+    name = ""
+    metric = ""
+    dtype = "bf16"
+    description = ""
+    dominant = ""
+    dominant_bytes = 0
+    bytes_per_step = 0
+    tokens_per_step = 0
+
+    def step(self, events: list | None) -> None:
+        raise NotImplementedError
+
+    def cpu_baseline(self) -> dict:
+        raise NotImplementedError
+
+
+class RMSNormWorkload(Workload):
+    name = "rmsnorm"
+    metric = HEADLINE_METRIC
+    rows, cols, eps = 16384, 4096, 1e-5
+
+    def __init__(self, layers: int) -> None:
+        self.layers = layers
+        r, c = self.rows, self.cols
+        self.w = _seeded((c,), torch.bfloat16, 2, 0.02, 1.0)
+        self.x = [_seeded((r, c), torch.bfloat16, 10 + i) for i in range(layers)]
+        self.dy = [_seeded((r, c), torch.bfloat16, 20 + i) for i in range(layers)]
+        self.y = [torch.empty_like(t) for t in self.x]
+        self.dx = [torch.empty_like(t) for t in self.x]
+        self.rstd = [torch.empty(r, dtype=torch.float32, device="cuda") for _ in range(layers)]
+        self.dw = [torch.empty(c, dtype=torch.bfloat16, device="cuda") for _ in range(layers)]
+        lib = _lib.lib()
+        self.ws_bytes = lib.pt_rmsnorm_bwd_workspace_bytes(r, c, _lib.PT_BFLOAT16)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
+        s, sw = 2, 2
+        self.fwd_bytes = 2 * r * c * s + c * sw + 4 * r
+        self.bwd_bytes = 3 * r * c * s + 2 * c * sw + 4 * r
+        self.bytes_per_step = layers * (self.fwd_bytes + self.bwd_bytes)
+        self.tokens_per_step = layers * r
+        self.dominant = "rmsnorm backward (rmsnorm_bwd_kernel row pass + rmsnorm_dw_finish_kernel)"
+        self.dominant_bytes = self.bwd_bytes
+        self.description = (
+            f"RMSNorm fwd+bwd bf16 [16384 tokens (8x2048), 4096], eps 1e-5, bf16 weight, fp32 rstd; "
+            f"step = forward of {layers} independent activations then backward in reverse"
+        )
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self._fwd = [
+            (lib.pt_rmsnorm_fwd, (_p(self.x[i]), c, _p(self.w), _p(self.y[i]), c, _p(self.rstd[i]),
+                                  r, c, ctypes.c_float(self.eps), _lib.PT_BFLOAT16, _lib.PT_BFLOAT16, stream))
+            for i in range(layers)
+        ]
+        self._bwd = [
+            (lib.pt_rmsnorm_bwd, (_p(self.dy[i]), c, _p(self.x[i]), c, _p(self.w), _p(self.rstd[i]),
+                                  _p(self.dx[i]), c, _p(self.dw[i]), _p(self.ws), self.ws_bytes, r, c,
+                                  _lib.PT_BFLOAT16, _lib.PT_BFLOAT16, stream))
+            for i in range(layers)
+        ]
+
+    def step(self, events):
+        for fn, args in self._fwd:
+            rc = fn(*args)
+            if rc:
+                _lib.check("pt_rmsnorm_fwd", rc)
+        for fn, args in reversed(self._bwd):
+            if events is not None:
+                start, end = events.pop()
+                start.record()
+            rc = fn(*args)
+            if events is not None:
+                end.record()
+            if rc:
+                _lib.check("pt_rmsnorm_bwd", rc)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import rmsnorm as o_rms
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        rows = 2048
+        x, dy, w = self.x[0][:rows].cpu(), self.dy[0][:rows].cpu(), self.w.cpu()
+        sec = _time_cpu(lambda: o_rms.fallback_forward_backward(x, w, self.eps, dy))
+        c = self.cols
+        nbytes = 5 * rows * c * 2 + 3 * c * 2 + 8 * rows
+        return dict(
+            value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"first {rows} of 16384 rows (1/8 of one activation): reference PyTorch fallback "
+                   f"fwd+bwd (rmsnorm.py:56-60,113-134) on bf16 CPU tensors, median of 3 after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=rows / sec,
+        )
+
+
+class SwiGLUWorkload(Workload):
+    name = "swiglu"
+    metric = "SwiGLU fwd+bwd HBM GB/s & % of peak, 16k tok×14336 bf16"
+    rows, cols = 16384, 14336
+
+    def __init__(self, layers: int) -> None:
+        self.layers = layers
+        n = self.rows * self.cols
+        self.n = n
+        self.g = [_seeded((n,), torch.bfloat16, 30 + i) for i in range(layers)]
+        self.u = [_seeded((n,), torch.bfloat16, 40 + i) for i in range(layers)]
+        self.dy = [_seeded((n,), torch.bfloat16, 50 + i) for i in range(layers)]
+        self.y = [torch.empty_like(t) for t in self.g]
+        self.dg = [torch.empty_like(t) for t in self.g]
+        self.du = [torch.empty_like(t) for t in self.g]
+        lib = _lib.lib()
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self.bytes_per_step = layers * 8 * n * 2
+        self.tokens_per_step = layers * self.rows
+        self.dominant = "swiglu_bwd_kernel"
+        self.dominant_bytes = 5 * n * 2
+        self.description = (
+            f"SwiGLU fwd+bwd bf16 gate/up [16384, 14336]; step = forward of {layers} independent "
+            f"activations then backward in reverse"
+        )
+        self._fwd = [(lib.pt_swiglu_fwd, (_p(self.g[i]), _p(self.u[i]), _p(self.y[i]), n, _lib.PT_BFLOAT16, stream))
+                     for i in range(layers)]
+        self._bwd = [(lib.pt_swiglu_bwd, (_p(self.dy[i]), _p(self.g[i]), _p(self.u[i]), _p(self.dg[i]),
+                                          _p(self.du[i]), n, _lib.PT_BFLOAT16, stream)) for i in range(layers)]
+
+    def step(self, events):
+        for fn, args in self._fwd:
+            if fn(*args):
+                _lib.check("pt_swiglu_fwd", 1)
+        for fn, args in reversed(self._bwd):
+            if events is not None:
+                start, end = events.pop()
+                start.record()
+            rc = fn(*args)
+            if events is not None:
+                end.record()
+            if rc:
+                _lib.check("pt_swiglu_bwd", rc)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import swiglu as o_swiglu
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        rows = 512
+        n = rows * self.cols
+        g, u, dy = self.g[0][:n].cpu(), self.u[0][:n].cpu(), self.dy[0][:n].cpu()
+        sec = _time_cpu(lambda: o_swiglu.fallback_forward_backward(g, u, dy))
+        return dict(
+            value=8 * n * 2 / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"first {rows} of 16384 token rows: reference PyTorch fallback fwd+bwd (F.silu*up, "
+                   f"swiglu.py:75-81) on bf16 CPU tensors, median of 3 after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=rows / sec,
+        )
+
+
+class RoPEWorkload(Workload):
+    name = "rope"
+    metric = "RoPE fwd+bwd HBM GB/s & % of peak, q[8,2048,32,128] k[8,2048,8,128] bf16"
+
+    def __init__(self, layers: int, layout: str = "rotate_half") -> None:
+        from picotron_amd.nn.rope import rotary_cos_sin
+
+        self.layers = layers
+        self.layout = layout
+        b, s, hq, hk, d = 8, 2048, 32, 8, 128
+        self.cos, self.sin = rotary_cos_sin(s, d, 500_000.0, device=torch.device("cuda"), dtype=torch.float32)
+        self.q = [_seeded((b, s, hq, d), torch.bfloat16, 60 + i).transpose(1, 2) for i in range(layers)]
+        self.k = [_seeded((b, s, hk, d), torch.bfloat16, 70 + i).transpose(1, 2) for i in range(layers)]
+        self.dq = [_seeded((b, s, hq, d), torch.bfloat16, 80 + i).transpose(1, 2) for i in range(layers)]
+        self.dk = [_seeded((b, s, hk, d), torch.bfloat16, 90 + i).transpose(1, 2) for i in range(layers)]
+        self.yq = [torch.empty_like(t) for t in self.q]
+        self.yk = [torch.empty_like(t) for t in self.k]
+        self.gq = [torch.empty_like(t) for t in self.q]
+        self.gk = [torch.empty_like(t) for t in self.k]
+        lib = _lib.lib()
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        qk_bytes = (b * s * hq * d + b * s * hk * d) * 2
+        self.bytes_per_step = layers * 4 * qk_bytes
+        self.tokens_per_step = layers * b * s
+        self.dominant = "rope_kernel (query + key forward, one launch)"
+        self.dominant_bytes = 2 * qk_bytes
+        self.description = (
+            f"RoPE fwd+bwd bf16 q [8,2048,32,128], k [8,2048,8,128] in (B,S,H,D) memory, {layout}, "
+            f"theta 5e5, fp32 cos/sin; step = forward of {layers} layers then backward in reverse"
+        )
+        lay = ops.LAYOUTS[layout]
+        self._keep = []
+
+        def call(x0, y0, x1, y1, inverse):
+            d0, d1 = ops._rope_desc(x0, y0), ops._rope_desc(x1, y1)
+            self._keep.extend([d0, d1])
+            return (lib.pt_rope, (_p(x0), _p(y0), d0, _p(x1), _p(y1), d1, d, _p(self.cos), _p(self.sin),
+                                  s, lay, inverse, _lib.PT_BFLOAT16, stream))
+
+        self._fwd = [call(self.q[i], self.yq[i], self.k[i], self.yk[i], 0) for i in range(layers)]
+        self._bwd = [call(self.dq[i], self.gq[i], self.dk[i], self.gk[i], 1) for i in range(layers)]
+
+    def step(self, events):
+        for fn, args in self._fwd:
+            if events is not None:
+                start, end = events.pop()
+                start.record()
+            rc = fn(*args)
+            if events is not None:
+                end.record()
+            if rc:
+                _lib.check("pt_rope", rc)
+        for fn, args in reversed(self._bwd):
+            rc = fn(*args)
+            if rc:
+                _lib.check("pt_rope", rc)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import rope as o_rope
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        bsz = 1
+        q = self.q[0][:bsz].cpu()
+        dq = self.dq[0][:bsz].cpu()
+        cos, sin = self.cos.cpu().bfloat16(), self.sin.cpu().bfloat16()
+        sec = _time_cpu(lambda: o_rope.fallback_forward_backward(q, cos, sin, dq))
+        nbytes = 4 * q.numel() * 2
+        return dict(
+            value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample="query of batch element 0 (1/8 of q): reference eager apply_rotary_embedding "
+                   "(rope.py:35-51, interleaved, bf16 tables) fwd + autograd bwd on CPU, median of 3",
+            seconds_per_call=sec, tokens_per_s=2048 / sec,
+        )
+
+
+class CrossEntropyWorkload(Workload):
+    name = "ce"
+    metric = "Fused cross-entropy fwd+bwd HBM GB/s & % of peak, [8192, 128256] bf16"
+    rows, vocab = 8192, 128256
+
+    def __init__(self, layers: int) -> None:
+        self.layers = 1
+        r, v = self.rows, self.vocab
+        self.logits = _seeded((r, v), torch.bfloat16, 100, 2.0)
+        g = torch.Generator(device="cuda").manual_seed(101)
+        self.targets = torch.randint(0, v, (r,), generator=g, device="cuda")
+        self.targets[torch.randperm(r, generator=g, device="cuda")[:410]] = -100
+        lib = _lib.lib()
+        self.ws_bytes = lib.pt_cross_entropy_workspace_bytes(r)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
+        self.loss = torch.empty((), dtype=torch.float32, device="cuda")
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self.bytes_per_step = 2 * r * v * 2 + 16 * r
+        self.tokens_per_step = r
+        self.dominant = "cross-entropy fused fwd+bwd (ce_prepare_kernel + ce_rows_kernel)"
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "fused cross-entropy fwd+bwd bf16 logits [8192, 128256] ~N(0,2^2), 410 targets = -100, "
+            "fp32 mean loss, dlogits written in place; step = one fused call (each step re-reads the "
+            "previous step's in-place output as its logits)"
+        )
+        self._call = (lib.pt_cross_entropy, (_p(self.logits), r, 1, v, 0, v, _p(self.targets), 1, 0, -100,
+                                             _p(self.loss), 1, _p(self.ws), self.ws_bytes, _lib.PT_BFLOAT16, stream))
+
+    def step(self, events):
+        fn, args = self._call
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        rc = fn(*args)
+        if events is not None:
+            end.record()
+        if rc:
+            _lib.check("pt_cross_entropy", rc)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import cross_entropy as o_ce
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        rows = 256
+        logits = _seeded((rows, self.vocab), torch.bfloat16, 100, 2.0).cpu()
+        targets = self.targets[:rows].cpu()
+        sec = _time_cpu(lambda: o_ce.fallback_forward_backward(logits, targets))
+        return dict(
+            value=(2 * rows * self.vocab * 2 + 16 * rows) / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"{rows} of 8192 rows: F.cross_entropy fwd + autograd bwd on the fp32 upcast (the "
+                   f"reference fallback under autocast), median of 3",
+            seconds_per_call=sec, tokens_per_s=rows / sec,
+        )
+
+
+class AdamWWorkload(Workload):
+    name = "adamw"
+    metric = "Fused AdamW step HBM GB/s & % of peak, 1.2e9 fp32 params"
+    dtype = "f32"
+    n = 1_200_000_000
+
+    def __init__(self, layers: int) -> None:
+        self.layers = 1
+        n = self.n
+        self.p = _seeded((n,), torch.float32, 110, 0.02)
+        self.g = _seeded((n,), torch.float32, 111, 1e-3)
+        self.m = torch.zeros(n, dtype=torch.float32, device="cuda")
+        self.v = torch.zeros(n, dtype=torch.float32, device="cuda")
+        host, blocks = ops.adamw_table([self.p], [self.g], [self.m], [self.v])
+        self.table = host.cuda()
+        self.blocks = blocks
+        self.t = 1
+        self.bytes_per_step = 28 * n
+        self.tokens_per_step = n
+        self.dominant = "adamw_kernel"
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "fused AdamW over one flat 1.2e9-element fp32 parameter (p, grad, exp_avg, exp_avg_sq), "
+            "lr 3e-4, betas (0.9, 0.95), eps 1e-8, wd 0.1; step = one optimizer step"
+        )
+        self.lib = _lib.lib()
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        rc = self.lib.pt_adamw_step(_p(self.table), 1, self.blocks, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                                    float(self.t), self.stream)
+        if events is not None:
+            end.record()
+        self.t += 1
+        if rc:
+            _lib.check("pt_adamw_step", rc)
+
+    def cpu_baseline(self) -> dict:
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        n = 50_000_000
+        p = torch.nn.Parameter(self.p[:n].cpu())
+        p.grad = self.g[:n].cpu()
+        opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+        sec = _time_cpu(opt.step)
+        return dict(
+            value=28 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"{n:.0e} of 1.2e9 params: torch.optim.AdamW(foreach=False).step() (the reference "
+                   f"fallback, adamw.py:47) on CPU, median of 3 after 1 warm-up",
+            seconds_per_call=sec, params_per_s=n / sec,
+        )
+
+
+class CopyWorkload(Workload):
+    name = "copy"
+    metric = "128-bit streaming copy HBM GB/s (achievable-bandwidth reference)"
+    dtype = "u8"
+    nbytes = 1 << 30
+
+    def __init__(self, layers: int) -> None:
+        self.layers = layers
+        self.src = [torch.empty(self.nbytes, dtype=torch.uint8, device="cuda").fill_(i) for i in range(layers)]
+        self.dst = [torch.empty(self.nbytes, dtype=torch.uint8, device="cuda") for _ in range(layers)]
+        self.bytes_per_step = layers * 2 * self.nbytes
+        self.tokens_per_step = 0
+        self.dominant = "copy16_kernel"
+        self.dominant_bytes = 2 * self.nbytes
+        self.description = f"pt_copy of {layers} x 1 GiB buffers (read + write)"
+        self.lib = _lib.lib()
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(self, events):
+        for s, d in zip(self.src, self.dst):
+            if events is not None:
+                start, end = events.pop()
+                start.record()
+            rc = self.lib.pt_copy(_p(s), _p(d), self.nbytes, self.stream)
+            if events is not None:
+                end.record()
+            if rc:
+                _lib.check("pt_copy", rc)
+
+    def cpu_baseline(self) -> dict:
+        return None
+
+
+WORKLOADS = {
+    "rmsnorm": RMSNormWorkload,
+    "swiglu": SwiGLUWorkload,
+    "rope": RoPEWorkload,
+    "ce": CrossEntropyWorkload,
+    "adamw": AdamWWorkload,
+    "copy": CopyWorkload,
+}
+
+DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "adamw": 1, "copy": 4}
+
+
+def _traffic(workload: str) -> dict | None:
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
+    summary (profiles/<workload>_traffic.json), if one exists."""
+
+    path = ROOT / "profiles" / f"{workload}_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    return data
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description="fused-kernel HBM benchmark (one MI355X)")
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="rmsnorm")
+    parser.add_argument("--layers", type=int, default=None)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the kernels run on a single MI355X and this build has "
+              "no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    _lib.lib()
+    if not ops.device_supported(0):
+        print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)
+        return 2
+
+    layers = args.layers or DEFAULT_LAYERS[args.workload]
+    wl = WORKLOADS[args.workload](layers)
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        wl.step(None)
+    torch.cuda.synchronize()
+
+    per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "adamw": 1, "copy": layers}[args.workload]
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps * per_step)]
+    pending = list(reversed(events))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.step(pending)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    ms_per_step = elapsed / args.steps * 1e3
+    gbps = wl.bytes_per_step / (elapsed / args.steps) / 1e9
+    launch_ms = [s.elapsed_time(e) for s, e in events]
+    avg_us = statistics.mean(launch_ms) * 1e3
+    achieved = wl.dominant_bytes / (avg_us * 1e-6) / 1e9
+    traffic = _traffic(args.workload)
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_GBPS, 4),
+        "traffic": traffic.get("bytes_per_launch") if traffic else None,
+        "kernel": wl.dominant,
+        "algorithmic_bytes_per_launch": wl.dominant_bytes,
+        "avg_launch_us": round(avg_us, 2),
+        "median_launch_us": round(statistics.median(launch_ms) * 1e3, 2),
+        "launches_timed": len(launch_ms),
+    }
+    if traffic:
+        roofline["traffic_source"] = traffic.get("source")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = wl.cpu_baseline()
+        if cpu is not None:
+            cores, ncpu, model = _cpu_info()
+            cpu.update(os_cpu_count=ncpu, cpu_model=model)
+            for key in ("value", "seconds_per_call", "tokens_per_s", "params_per_s"):
+                if key in cpu:
+                    cpu[key] = round(cpu[key], 4) if key == "seconds_per_call" else round(cpu[key], 2)
+
+    result = {
+        "metric": wl.metric,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.dtype,
+        "data": "synthetic (seeded on device)",
+        "config": {
+            "workload": wl.description,
+            "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+            "algorithmic_bytes_per_step": wl.bytes_per_step,
+            "tokens_per_step": wl.tokens_per_step,
+            "tokens_per_s": round(wl.tokens_per_step / (elapsed / args.steps), 1),
+            "layers_per_step": layers,
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

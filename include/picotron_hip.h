@@ -1,0 +1,183 @@
+/*
+ * picotron_hip.h -- C ABI of libpicotron_hip.so, the gfx950 (MI355X) kernels behind
+ * picotron's optional fused-kernel surface (picotron.nn.triton_kernels).
+ *
+ * Every entry point is extern "C", takes plain device pointers, element counts and
+ * strides, and an explicit HIP stream (passed as void*; NULL means the default stream).
+ * The library never allocates or frees device memory: the caller owns every buffer,
+ * including workspaces, whose sizes the *_workspace_bytes() queries return.
+ *
+ * Return value: PT_OK (0) on success, otherwise a PT_E* code; pt_last_error() then
+ * returns a message for the calling thread.  Validation happens on the host before
+ * any launch, so a nonzero return means nothing was enqueued.  Asynchronous device
+ * faults are not reported here (as with any HIP launch).
+ *
+ * Strides and counts are in ELEMENTS, not bytes.  The innermost (hidden / head_dim /
+ * vocab) dimension must be contiguous (stride 1).
+ *
+ * Reference interfaces (AndyMLAndAI/picotron) that these entry points replace are
+ * cited as path:line relative to the reference repository root.
+ */
+#ifndef PICOTRON_HIP_H
+#define PICOTRON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PT_ABI_VERSION 1
+
+/* element type codes (storage types; arithmetic is always fp32) */
+#define PT_FLOAT32 0
+#define PT_FLOAT16 1
+#define PT_BFLOAT16 2
+
+/* return codes */
+#define PT_OK 0
+#define PT_EINVAL 1        /* bad argument: null pointer, shape, stride, alignment */
+#define PT_EUNSUPPORTED 2  /* valid request this build does not handle (dtype, size) */
+#define PT_ELAUNCH 3       /* hipGetLastError() reported a launch failure */
+#define PT_EDEVICE 4       /* no usable gfx950 device / HIP runtime error */
+
+/* ABI version of the loaded library; must equal PT_ABI_VERSION. */
+int pt_abi_version(void);
+
+/* Message for the last nonzero return on the calling thread ("" if none). */
+const char* pt_last_error(void);
+
+/* 1 if `device` is a gfx950 GPU this library was built for, 0 otherwise.
+ * Replaces the capability gate of src/picotron/utils/hardware.py:93-108
+ * (detect_triton_support: capability >= 7) and the per-op checks at
+ * src/picotron/nn/triton_kernels/rmsnorm.py:185-186, swiglu.py:303-304. */
+int pt_device_supported(int device);
+
+/* ---------------------------------------------------------------- RMSNorm
+ * y[r, :] = (x[r, :] * rstd[r]) * w,   rstd[r] = 1 / sqrt(mean(x[r, :]^2) + eps)
+ * computed in fp32, stored in x's type; rstd is written in fp32 for the backward.
+ * Replaces _rmsnorm_kernel + _run_triton_forward (src/picotron/nn/triton_kernels/
+ * rmsnorm.py:25-46, 63-84) and _inverse_rms (rmsnorm.py:49-53), which the reference
+ * runs as a separate full pass on every forward (rmsnorm.py:103).
+ * x_dtype: type of x and y.  w_dtype: type of weight (any of the three). */
+int pt_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* weight, void* y,
+                   int64_t y_row_stride, float* rstd, int64_t rows, int64_t cols, float eps,
+                   int x_dtype, int w_dtype, void* stream);
+
+/* Bytes of fp32 workspace pt_rmsnorm_bwd needs for the weight-gradient partials. */
+size_t pt_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols, int x_dtype);
+
+/* dx = rstd * (dy*w - x * rstd^2 * mean(dy*w*x)),  dweight = sum_rows(dy * x * rstd)
+ * Replaces the PyTorch-eager backward of _RMSNormAutogradFunction
+ * (src/picotron/nn/triton_kernels/rmsnorm.py:110-134).  dx may be NULL (no input grad);
+ * dweight may be NULL (no weight grad; workspace then unused).  dy has x's type, dx is
+ * written in x's type and dweight in w's type.  The weight reduction is deterministic:
+ * per-block fp32 partials in `workspace`, then a fixed-order column sum. */
+int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t x_row_stride,
+                   const void* weight, const float* rstd, void* dx, int64_t dx_row_stride,
+                   void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
+                   int64_t cols, int x_dtype, int w_dtype, void* stream);
+
+/* ---------------------------------------------------------------- SwiGLU
+ * out = gate * sigmoid(gate) * up over n contiguous elements (fp32 math).
+ * Replaces _swiglu_kernel + _run_triton_forward (src/picotron/nn/triton_kernels/
+ * swiglu.py:26-53). */
+int pt_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dtype,
+                  void* stream);
+
+/* s = sigmoid(g); dgate = dout * up * s * (1 + g * (1 - s)); dup = dout * g * s.
+ * Replaces the eager backward of _SwiGLUAutogradFunction (swiglu.py:71-81), computed
+ * in fp32 instead of the input type.  dgate or dup may be NULL to skip that output. */
+int pt_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dgate, void* dup,
+                  int64_t n, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- RoPE
+ * Rotary embedding of up to two tensors (query and key) in one launch.  Each tensor is a
+ * logical (batch, heads, seq, head_dim) view described by
+ *   desc[9] = {batch, heads, seq, x_stride_batch, x_stride_head, x_stride_seq,
+ *              y_stride_batch, y_stride_head, y_stride_seq}
+ * with head_dim contiguous.  Position of sequence index s is table row s; cos_table and
+ * sin_table are fp32 [table_rows, head_dim/2] (table_rows >= seq).
+ * layout 0 = interleaved pairs (2i, 2i+1), as in src/picotron/nn/rope.py:35-51 and the
+ *            Triton kernel src/picotron/nn/triton_kernels/rope.py:25-49;
+ * layout 1 = rotate-half pairs (i, i + head_dim/2).
+ * inverse = 1 rotates by -angle (the backward of the forward rotation).
+ * x1/y1/desc1 may be NULL for a single tensor.  y may alias x (in place).
+ * Replaces triton_apply_rotary_embedding (src/picotron/nn/triton_kernels/rope.py:52-91)
+ * and, through autograd, the eager apply_rotary_embedding backward. */
+int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void* y1,
+            const int64_t* desc1, int64_t head_dim, const float* cos_table,
+            const float* sin_table, int64_t table_rows, int layout, int inverse, int dtype,
+            void* stream);
+
+/* ---------------------------------------------------------------- Cross-entropy
+ * Mean cross-entropy over rows whose target != ignore_index, fused with its gradient.
+ * Row (o, i), o < outer, i < inner, starts at logits + o*outer_stride + i*inner_stride
+ * and holds `vocab` contiguous logits; its target is
+ * targets[o*t_outer_stride + i*t_inner_stride] (int64).  A 2-D (N, V) input is
+ * outer=N, inner=1; the train loop's (B, V, S-1) view of (B, S, V) logits is
+ * outer=B, inner=S-1, outer_stride=S*V, inner_stride=V.
+ * loss_out (fp32 scalar, device) = sum(lse - logit[target]) / n_valid.
+ * If write_grad != 0 the logits are overwritten IN PLACE with
+ *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows).
+ * A non-ignored target outside [0, vocab) makes that row's loss NaN and sets
+ * *(int32*)status bit 0; status is part of the workspace (see below).
+ * Replaces CrossEntropyWithFallback / triton_cross_entropy
+ * (src/picotron/nn/triton_kernels/cross_entropy.py:48-109) and the F.cross_entropy
+ * fwd+bwd they fall back to. */
+size_t pt_cross_entropy_workspace_bytes(int64_t rows);
+int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_stride,
+                     int64_t inner_stride, int64_t vocab, const int64_t* targets,
+                     int64_t t_outer_stride, int64_t t_inner_stride, int64_t ignore_index,
+                     float* loss_out, int write_grad, void* workspace, size_t workspace_bytes,
+                     int dtype, void* stream);
+
+/* Device address of the int32 status word inside a cross-entropy workspace. */
+int32_t* pt_cross_entropy_status(void* workspace);
+
+/* Multiply a gradient written by pt_cross_entropy (same row and target description) by
+ * the fp32 scalar at *grad_output (device memory), skipping all work when it equals 1.0
+ * exactly; rows whose target is ignore_index stay zero.  This is the backward of the fused
+ * loss: the logits already hold d(mean loss)/d(logits). */
+int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
+                                int64_t outer_stride, int64_t inner_stride, int64_t vocab,
+                                const int64_t* targets, int64_t t_outer_stride,
+                                int64_t t_inner_stride, int64_t ignore_index,
+                                const float* grad_output, int dtype, void* stream);
+
+/* ---------------------------------------------------------------- AdamW
+ * One decoupled-weight-decay Adam step over many fp32 tensors in one launch, with
+ * torch.optim.AdamW's single-tensor arithmetic (amsgrad=False, maximize=False), per element:
+ *   p *= 1 - lr*wd;  m = lerp(m, g, 1-beta1);  v = v*beta2 + ((1-beta2)*g)*g;
+ *   p += -step_size * (m / (sqrt(v) / bias_correction2_sqrt + eps))
+ * The library derives step_size = lr / (1 - beta1^step) and
+ * bias_correction2_sqrt = (1 - beta2^step)^0.5 in double from the arguments (as torch does
+ * in Python floats) and rounds every scalar to fp32 once.  `step` is the step number AFTER
+ * the increment (1 on the first step).
+ * `table` is a DEVICE array of n_tensors records of 6 int64:
+ *   {param address, grad address, exp_avg address, exp_avg_sq address, numel,
+ *    first block index}
+ * where "first block index" is the running sum of ceil(numel / pt_adamw_block_elems())
+ * over the preceding records (so record 0 has 0); total_blocks is the sum over all
+ * records.  Every record must have numel >= 1.
+ * Replaces triton_adamw_step / AdamWStepWithFallback
+ * (src/picotron/nn/triton_kernels/adamw.py:14-47), which always raises today, and the
+ * torch.optim.AdamW step it falls back to (src/picotron/training/train_loop.py:308-325). */
+int64_t pt_adamw_block_elems(void);
+int pt_adamw_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks, double lr,
+                  double beta1, double beta2, double eps, double weight_decay, double step,
+                  void* stream);
+
+/* ---------------------------------------------------------------- Utility
+ * Device-to-device copy of `bytes` (multiple of 16, 16-byte aligned pointers) with the
+ * same 128-bit load/store pattern as the streaming kernels.  No reference counterpart:
+ * used by the benchmark as the achievable-bandwidth line and to calibrate rocprofv3
+ * FETCH_SIZE / WRITE_SIZE against a transfer of known size. */
+int pt_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PICOTRON_HIP_H */

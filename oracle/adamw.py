@@ -1,0 +1,46 @@
+"""AdamW oracle (test infrastructure; see oracle/__init__.py).
+
+Reference: src/picotron/nn/triton_kernels/adamw.py:34-47 falls back to optimizer.step() of
+torch.optim.AdamW(params, lr, betas, eps, weight_decay) (train_loop.py:308-325), i.e.
+torch's single-tensor Adam with decoupled weight decay, amsgrad=False:
+  p *= 1 - lr*wd; m = lerp(m, g, 1-b1); v = v*b2 + (1-b2)*g*g;
+  p -= (lr / (1 - b1^t)) * m / (sqrt(v) / sqrt(1 - b2^t) + eps)
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+
+def step(
+    p: Tensor,
+    g: Tensor,
+    m: Tensor,
+    v: Tensor,
+    *,
+    t: int,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    compute: torch.dtype = torch.float64,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """One step from state (m, v) at step t-1 to step t; returns new (p, m, v) in compute."""
+
+    pc, gc, mc, vc = (x.to(compute) for x in (p, g, m, v))
+    pc = pc * (1 - lr * weight_decay)
+    mc = mc + (1 - beta1) * (gc - mc)
+    vc = vc * beta2 + (1 - beta2) * gc * gc
+    bc1 = 1 - beta1**t
+    bc2 = 1 - beta2**t
+    denom = torch.sqrt(vc) / (bc2**0.5) + eps
+    pc = pc - (lr / bc1) * mc / denom
+    return pc, mc, vc
+
+
+def fallback_step(optimizer: torch.optim.Optimizer) -> None:
+    """The reference's fallback as it runs: torch's own AdamW step."""
+
+    optimizer.step()

@@ -1,0 +1,104 @@
+// Library-wide C ABI: version, per-thread error message, device gate, and the
+// 128-bit streaming copy used as the achievable-bandwidth reference.
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "pt_common.hpp"
+
+namespace pt {
+
+namespace {
+thread_local std::string g_last_error;
+
+constexpr int kMaxDevices = 64;
+int g_cus[kMaxDevices];
+std::once_flag g_cus_once[kMaxDevices];
+}  // namespace
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return PT_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return fail(PT_ELAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+  }
+  return ok();
+}
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::call_once(g_cus_once[dev], [dev] {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0) {
+      n = 256;
+    }
+    g_cus[dev] = n;
+  });
+  return g_cus[dev];
+}
+
+// Grid-stride 16-byte copy; UNROLL independent vectors in flight per thread.
+template <int UNROLL>
+__global__ __launch_bounds__(256) void copy16_kernel(const u32x4* __restrict__ src,
+                                                     u32x4* __restrict__ dst, int64_t nvec) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * UNROLL;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * UNROLL + threadIdx.x;
+       base < nvec; base += stride) {
+    u32x4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
+      if (i < nvec) v[u] = __builtin_nontemporal_load(src + i);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
+      if (i < nvec) __builtin_nontemporal_store(v[u], dst + i);
+    }
+  }
+}
+
+}  // namespace pt
+
+extern "C" {
+
+int pt_abi_version(void) { return PT_ABI_VERSION; }
+
+const char* pt_last_error(void) { return pt::g_last_error.c_str(); }
+
+int pt_device_supported(int device) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+  return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int pt_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  if (src == nullptr || dst == nullptr) return pt::fail(PT_EINVAL, "pt_copy: null pointer");
+  if (bytes < 0 || (bytes & 15) != 0)
+    return pt::fail(PT_EINVAL, "pt_copy: bytes must be a non-negative multiple of 16");
+  if (!pt::aligned16(src) || !pt::aligned16(dst))
+    return pt::fail(PT_EINVAL, "pt_copy: pointers must be 16-byte aligned");
+  if (bytes == 0) return pt::ok();
+  constexpr int kUnroll = 4;
+  const int64_t nvec = bytes / 16;
+  int64_t blocks = (nvec + 256 * kUnroll - 1) / (256 * kUnroll);
+  const int64_t cap = static_cast<int64_t>(pt::num_cus()) * 32;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(pt::copy16_kernel<kUnroll>, dim3(static_cast<unsigned>(blocks)), dim3(256),
+                     0, pt::as_stream(stream), reinterpret_cast<const pt::u32x4*>(src),
+                     reinterpret_cast<pt::u32x4*>(dst), nvec);
+  return pt::check_launch("pt_copy");
+}
+
+}  // extern "C"

@@ -1,0 +1,167 @@
+// Shared device and host helpers for the gfx950 kernels of libpicotron_hip.so.
+//
+// Storage types are fp32, fp16 and bf16; all arithmetic is fp32.  Global memory is
+// moved in 16-byte (128-bit) vectors wherever the caller's pointers and strides allow
+// it, so one wave64 instruction moves 1 KiB of contiguous data.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/picotron_hip.h"
+
+namespace pt {
+
+// ------------------------------------------------------------------ host-side errors
+
+// Records `msg` as the calling thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Clears the calling thread's last error and returns PT_OK.
+int ok();
+// Checks the last HIP launch; returns PT_OK or PT_ELAUNCH with the HIP message.
+int check_launch(const char* what);
+// Number of compute units of the current device (cached per device).
+int num_cus();
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int dtype_size(int dtype) { return dtype == PT_FLOAT32 ? 4 : 2; }
+inline bool valid_dtype(int dtype) {
+  return dtype == PT_FLOAT32 || dtype == PT_FLOAT16 || dtype == PT_BFLOAT16;
+}
+
+// ------------------------------------------------------------------ device types
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Storage-type traits.  VEC = elements per 16-byte vector.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int VEC = 4;
+  static __device__ __forceinline__ float to_f32(float v) { return v; }
+  static __device__ __forceinline__ float from_f32(float v) { return v; }
+};
+
+template <>
+struct Elem<_Float16> {
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f32(_Float16 v) { return static_cast<float>(v); }
+  // fptrunc is round-to-nearest-even, the same rounding as torch's .to(torch.float16).
+  static __device__ __forceinline__ _Float16 from_f32(float v) { return static_cast<_Float16>(v); }
+};
+
+template <>
+struct Elem<__bf16> {
+  static constexpr int VEC = 8;
+  static __device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
+  // Lowers to gfx950's v_cvt_pk_bf16_f32: round-to-nearest-even, NaN preserved, the
+  // same rounding as torch's .to(torch.bfloat16).
+  static __device__ __forceinline__ __bf16 from_f32(float v) { return static_cast<__bf16>(v); }
+};
+
+// A 16-byte vector of storage elements, viewed either as raw 32-bit words (for the
+// 128-bit global load/store) or as elements.
+template <typename T>
+union Vec16 {
+  u32x4 raw;
+  T e[16 / sizeof(T)];
+};
+
+// Loads 16 bytes from `p` (16-byte aligned).  NT selects a nontemporal access, used
+// for data that is touched exactly once (streams far larger than L2 + MALL).
+template <bool NT>
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(q);
+  } else {
+    return *q;
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void store16(void* p, u32x4 v) {
+  u32x4* q = reinterpret_cast<u32x4*>(p);
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, q);
+  } else {
+    *q = v;
+  }
+}
+
+// Loads VEC consecutive elements of storage type T as fp32.  ALIGNED: one 16-byte load
+// (caller guarantees alignment and that all VEC elements are in range); otherwise
+// element-wise loads of the first `valid` elements, zero-filling the rest.
+template <typename T, bool ALIGNED, bool NT = false>
+__device__ __forceinline__ void load_f32(const T* p, float (&out)[Elem<T>::VEC], int valid) {
+  constexpr int V = Elem<T>::VEC;
+  if constexpr (ALIGNED) {
+    Vec16<T> v;
+    v.raw = load16<NT>(p);
+#pragma unroll
+    for (int i = 0; i < V; ++i) out[i] = Elem<T>::to_f32(v.e[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) out[i] = (i < valid) ? Elem<T>::to_f32(p[i]) : 0.0f;
+  }
+}
+
+template <typename T, bool ALIGNED, bool NT = false>
+__device__ __forceinline__ void store_f32(T* p, const float (&in)[Elem<T>::VEC], int valid) {
+  constexpr int V = Elem<T>::VEC;
+  if constexpr (ALIGNED) {
+    Vec16<T> v;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v.e[i] = Elem<T>::from_f32(in[i]);
+    store16<NT>(p, v.raw);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (i < valid) p[i] = Elem<T>::from_f32(in[i]);
+  }
+}
+
+// Loads one element of a runtime-typed array as fp32 (weights: tiny, cache-resident).
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == PT_FLOAT32) return reinterpret_cast<const float*>(p)[i];
+  if (dtype == PT_BFLOAT16) return static_cast<float>(reinterpret_cast<const __bf16*>(p)[i]);
+  return static_cast<float>(reinterpret_cast<const _Float16*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float v) {
+  if (dtype == PT_FLOAT32) {
+    reinterpret_cast<float*>(p)[i] = v;
+  } else if (dtype == PT_BFLOAT16) {
+    reinterpret_cast<__bf16*>(p)[i] = static_cast<__bf16>(v);
+  } else {
+    reinterpret_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+  }
+}
+
+// ------------------------------------------------------------------ reductions
+
+// Butterfly sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
+}
+
+constexpr int kWave = 64;
+
+}  // namespace pt

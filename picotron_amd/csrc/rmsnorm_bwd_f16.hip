@@ -1,0 +1,8 @@
+// RMSNorm backward launcher instantiated for _Float16 storage (kernels in rmsnorm_impl.hpp).
+#include "rmsnorm_impl.hpp"
+
+namespace pt {
+namespace rmsnorm {
+template void launch_bwd<_Float16>(const BwdArgs&);
+}  // namespace rmsnorm
+}  // namespace pt

@@ -1,0 +1,8 @@
+// RMSNorm forward launcher instantiated for float storage (kernels in rmsnorm_impl.hpp).
+#include "rmsnorm_impl.hpp"
+
+namespace pt {
+namespace rmsnorm {
+template void launch_fwd<float>(const FwdArgs&);
+}  // namespace rmsnorm
+}  // namespace pt

@@ -1,0 +1,261 @@
+// Rotary position embedding (forward and its inverse, the backward) for gfx950.
+//
+// Reference semantics (AndyMLAndAI/picotron):
+//   tables   src/picotron/nn/rope.py:13-32    angle[s, i] = s * theta^(-2i/D); cos/sin
+//   rotation src/picotron/nn/rope.py:35-51    interleaved pairs (2i, 2i+1):
+//            (a, b) -> (a*c - b*s, a*s + b*c)
+//   Triton   src/picotron/nn/triton_kernels/rope.py:25-49 (same pairs, forward only)
+// The rotate-half layout pairs (i, i + D/2) with the same angle table.  The inverse
+// rotation (a, b) -> (a*c + b*s, -a*s + b*c) is the exact transpose of the forward, so it
+// is the backward of the forward.
+//
+// Work item = one 16-byte vector of a row (interleaved: V/2 pairs) or one vector from each
+// half of a row (rotate-half: V pairs).  Rows are the (batch, head, seq) positions of a
+// strided view whose head_dim is contiguous; the host orders the three row dimensions by
+// decreasing stride so consecutive work items walk memory in address order.  Query and key
+// are handled by one launch (blocks [0, nb0) and [nb0, nb0 + nb1)).
+#include "pt_common.hpp"
+
+namespace pt {
+namespace {
+
+// Work items per row: interleaved rows split into V-element vectors (V/2 pairs each, or one
+// pair on the element path); rotate-half rows into P-pair groups taken from both halves.
+template <typename T, int LAYOUT, bool ALIGNED>
+__host__ __device__ constexpr int items_per_row(int head_dim) {
+  return LAYOUT == 0 ? head_dim / (ALIGNED ? Elem<T>::VEC : 2)
+                     : (head_dim / 2) / (ALIGNED ? Elem<T>::VEC : 1);
+}
+
+struct RopeTensor {
+  const void* x;
+  void* y;
+  int64_t n[3];    // row dimensions, outer to inner (iteration order)
+  int64_t xs[3];   // x strides of those dimensions (elements)
+  int64_t ys[3];   // y strides
+  int seq_dim;     // which of the three is the sequence dimension
+  int64_t rows;    // n[0] * n[1] * n[2]
+  int64_t items;   // rows * items_per_row
+  int64_t blocks;  // blocks assigned to this tensor
+};
+
+template <typename T, int LAYOUT, bool ALIGNED>
+__device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int head_dim,
+                                          const float* __restrict__ cos_t,
+                                          const float* __restrict__ sin_t, float sign) {
+  constexpr int V = ALIGNED ? Elem<T>::VEC : 2;
+  const int half = head_dim / 2;
+  const int per_row = items_per_row<T, LAYOUT, ALIGNED>(head_dim);
+  const int64_t row = item / per_row;
+  const int j = static_cast<int>(item - row * per_row);
+  int64_t idx[3];
+  idx[2] = row % t.n[2];
+  const int64_t r1 = row / t.n[2];
+  idx[1] = r1 % t.n[1];
+  idx[0] = r1 / t.n[1];
+  const int64_t xo = idx[0] * t.xs[0] + idx[1] * t.xs[1] + idx[2] * t.xs[2];
+  const int64_t yo = idx[0] * t.ys[0] + idx[1] * t.ys[1] + idx[2] * t.ys[2];
+  const int64_t s = idx[t.seq_dim];
+  const T* xr = static_cast<const T*>(t.x) + xo;
+  T* yr = static_cast<T*>(t.y) + yo;
+  const float* cr = cos_t + s * half;
+  const float* sr = sin_t + s * half;
+
+  if constexpr (LAYOUT == 0) {
+    // elements [j*V, j*V + V) = pairs [j*V/2, j*V/2 + V/2)
+    float a[V];
+    if constexpr (ALIGNED) {
+      load_f32<T, true>(xr + j * V, a, V);
+    } else {
+      a[0] = Elem<T>::to_f32(xr[2 * j]);
+      a[1] = Elem<T>::to_f32(xr[2 * j + 1]);
+    }
+    float o[V];
+#pragma unroll
+    for (int p = 0; p < V / 2; ++p) {
+      const int i = j * (V / 2) + p;
+      const float c = cr[i];
+      const float sn = sign * sr[i];
+      const float e = a[2 * p], od = a[2 * p + 1];
+      o[2 * p] = e * c - od * sn;
+      o[2 * p + 1] = e * sn + od * c;
+    }
+    if constexpr (ALIGNED) {
+      store_f32<T, true>(yr + j * V, o, V);
+    } else {
+      yr[2 * j] = Elem<T>::from_f32(o[0]);
+      yr[2 * j + 1] = Elem<T>::from_f32(o[1]);
+    }
+  } else {
+    constexpr int P = ALIGNED ? Elem<T>::VEC : 1;  // pairs per item
+    float a[P], b[P];
+    if constexpr (ALIGNED) {
+      load_f32<T, true>(xr + j * P, a, P);
+      load_f32<T, true>(xr + half + j * P, b, P);
+    } else {
+      a[0] = Elem<T>::to_f32(xr[j]);
+      b[0] = Elem<T>::to_f32(xr[half + j]);
+    }
+    float oa[P], ob[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int i = j * P + p;
+      const float c = cr[i];
+      const float sn = sign * sr[i];
+      oa[p] = a[p] * c - b[p] * sn;
+      ob[p] = a[p] * sn + b[p] * c;
+    }
+    if constexpr (ALIGNED) {
+      store_f32<T, true>(yr + j * P, oa, P);
+      store_f32<T, true>(yr + half + j * P, ob, P);
+    } else {
+      yr[j] = Elem<T>::from_f32(oa[0]);
+      yr[half + j] = Elem<T>::from_f32(ob[0]);
+    }
+  }
+}
+
+template <typename T, int LAYOUT, bool ALIGNED>
+__global__ __launch_bounds__(256) void rope_kernel(RopeTensor t0, RopeTensor t1, int head_dim,
+                                                   const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t, float sign) {
+  int64_t b = blockIdx.x;
+  const RopeTensor* t = &t0;
+  if (b >= t0.blocks) {
+    b -= t0.blocks;
+    t = &t1;
+  }
+  const int64_t item = b * 256 + threadIdx.x;
+  if (item >= t->items) return;
+  rope_item<T, LAYOUT, ALIGNED>(*t, item, head_dim, cos_t, sin_t, sign);
+}
+
+bool parse(const void* x, void* y, const int64_t* d, int64_t head_dim, int64_t table_rows,
+           int esize, int layout, RopeTensor* t, bool* aligned, std::string* err) {
+  const int64_t sz[3] = {d[0], d[1], d[2]};  // batch, heads, seq
+  const int64_t xs[3] = {d[3], d[4], d[5]};
+  const int64_t ys[3] = {d[6], d[7], d[8]};
+  for (int i = 0; i < 3; ++i) {
+    if (sz[i] < 0) {
+      *err = "negative dimension";
+      return false;
+    }
+  }
+  if (sz[2] > table_rows) {
+    *err = "sequence length exceeds the cos/sin table rows";
+    return false;
+  }
+  // iteration order: dimensions by decreasing x stride (stable), so the innermost
+  // iterated dimension has the smallest stride.
+  int ord[3] = {0, 1, 2};
+  for (int a = 0; a < 3; ++a)
+    for (int b = a + 1; b < 3; ++b)
+      if (xs[ord[b]] > xs[ord[a]]) {
+        const int tmp = ord[a];
+        ord[a] = ord[b];
+        ord[b] = tmp;
+      }
+  t->x = x;
+  t->y = y;
+  for (int i = 0; i < 3; ++i) {
+    t->n[i] = sz[ord[i]];
+    t->xs[i] = xs[ord[i]];
+    t->ys[i] = ys[ord[i]];
+    if (ord[i] == 2) t->seq_dim = i;
+  }
+  t->rows = sz[0] * sz[1] * sz[2];
+  // 16-byte vectors need aligned bases, strides that keep every row aligned, and
+  // (rotate-half) a half that is a whole number of vectors.
+  const int vec = 16 / esize;
+  bool al = aligned16(x) && aligned16(y) && head_dim % (2 * vec) == 0;
+  for (int i = 0; i < 3; ++i) {
+    if (sz[i] > 1 && ((xs[i] * esize) % 16 != 0 || (ys[i] * esize) % 16 != 0)) al = false;
+  }
+  if (layout == 0 && head_dim % vec != 0) al = false;
+  *aligned = al;
+  return true;
+}
+
+template <typename T, int LAYOUT, bool ALIGNED>
+void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const float* s,
+            float sign, hipStream_t st) {
+  const int per_row = items_per_row<T, LAYOUT, ALIGNED>(head_dim);
+  t0.items = t0.rows * per_row;
+  t1.items = t1.rows * per_row;
+  t0.blocks = (t0.items + 255) / 256;
+  t1.blocks = (t1.items + 255) / 256;
+  const int64_t blocks = t0.blocks + t1.blocks;
+  if (blocks == 0) return;
+  // pt_rope has checked that (rows0 + rows1) * head_dim / 2 + 512 < 2^32, which bounds
+  // blocks * 256 for every layout.
+  hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+}
+
+template <typename T>
+void launch_t(int layout, bool aligned, RopeTensor& t0, RopeTensor& t1, int head_dim,
+              const float* c, const float* s, float sign, hipStream_t st) {
+  if (layout == 0) {
+    if (aligned) {
+      launch<T, 0, true>(t0, t1, head_dim, c, s, sign, st);
+    } else {
+      launch<T, 0, false>(t0, t1, head_dim, c, s, sign, st);
+    }
+  } else {
+    if (aligned) {
+      launch<T, 1, true>(t0, t1, head_dim, c, s, sign, st);
+    } else {
+      launch<T, 1, false>(t0, t1, head_dim, c, s, sign, st);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace pt
+
+using namespace pt;
+
+extern "C" {
+
+int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void* y1,
+            const int64_t* desc1, int64_t head_dim, const float* cos_table,
+            const float* sin_table, int64_t table_rows, int layout, int inverse, int dtype,
+            void* stream) {
+  if (!valid_dtype(dtype)) return fail(PT_EINVAL, "pt_rope: unknown dtype code");
+  if (layout != 0 && layout != 1) return fail(PT_EINVAL, "pt_rope: layout must be 0 or 1");
+  if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > (1 << 20))
+    return fail(PT_EINVAL, "pt_rope: head_dim must be a positive even number");
+  if (!cos_table || !sin_table) return fail(PT_EINVAL, "pt_rope: null cos/sin table");
+  if (!x0 || !y0 || !desc0) return fail(PT_EINVAL, "pt_rope: null first tensor");
+  if ((x1 == nullptr) != (y1 == nullptr) || (x1 != nullptr && desc1 == nullptr))
+    return fail(PT_EINVAL, "pt_rope: second tensor needs x, y and desc");
+  const int esize = dtype_size(dtype);
+  RopeTensor t0{}, t1{};
+  bool al0 = true, al1 = true;
+  std::string err;
+  if (!parse(x0, y0, desc0, head_dim, table_rows, esize, layout, &t0, &al0, &err))
+    return fail(PT_EINVAL, "pt_rope: first tensor: " + err);
+  if (x1 != nullptr) {
+    if (!parse(x1, y1, desc1, head_dim, table_rows, esize, layout, &t1, &al1, &err))
+      return fail(PT_EINVAL, "pt_rope: second tensor: " + err);
+  } else {
+    t1.n[0] = t1.n[1] = t1.n[2] = 1;
+    t1.rows = 0;
+  }
+  const bool aligned = al0 && al1;
+  if ((t0.rows + t1.rows) * (head_dim / 2) + 512 > 0xffffffffLL)
+    return fail(PT_EUNSUPPORTED, "pt_rope: too many rows for one launch");
+  const float sign = inverse ? -1.0f : 1.0f;
+  hipStream_t st = as_stream(stream);
+  const int hd = static_cast<int>(head_dim);
+  if (dtype == PT_FLOAT32) {
+    launch_t<float>(layout, aligned, t0, t1, hd, cos_table, sin_table, sign, st);
+  } else if (dtype == PT_FLOAT16) {
+    launch_t<_Float16>(layout, aligned, t0, t1, hd, cos_table, sin_table, sign, st);
+  } else {
+    launch_t<__bf16>(layout, aligned, t0, t1, hd, cos_table, sin_table, sign, st);
+  }
+  return check_launch("pt_rope");
+}
+
+}  // extern "C"

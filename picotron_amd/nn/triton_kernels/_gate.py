@@ -1,0 +1,36 @@
+"""Shared launch gate for the fused kernels: library loaded, GPU tensors, gfx950 device.
+
+Replaces the Triton checks of the reference (``_TRITON_AVAILABLE``, ``is_cuda``,
+``get_device_capability(...)[0] >= 7``; e.g. src/picotron/nn/triton_kernels/rmsnorm.py:181-186).
+Each op passes its own ``*Unavailable`` exception type, so callers keep catching what the
+reference raised.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+from torch import Tensor
+
+from picotron_amd import _lib, ops
+
+# PICOTRON_HIP_DISABLE=1 makes every fused op report itself unavailable (forces the
+# PyTorch fallbacks, e.g. to compare against them on a GPU host).
+_DISABLED_ENV = "PICOTRON_HIP_DISABLE"
+
+
+def require_hip(exc: type[RuntimeError], op: str, *tensors: Tensor) -> None:
+    if os.environ.get(_DISABLED_ENV, "") not in ("", "0"):
+        raise exc(f"HIP {op} disabled by {_DISABLED_ENV}.")
+    reason = _lib.unavailable_reason()
+    if reason is not None:
+        raise exc(f"HIP kernel library unavailable: {reason}")
+    for t in tensors:
+        if not t.is_cuda:
+            raise exc(f"HIP {op} requires GPU tensors.")
+    index = tensors[0].device.index
+    if index is None:
+        index = torch.cuda.current_device()
+    if not ops.device_supported(index):
+        raise exc(f"HIP {op} requires a gfx950 (MI355X) device.")

@@ -1,0 +1,113 @@
+"""Fused cross-entropy forward + backward on gfx950 behind picotron's Triton-CE surface.
+
+Drop-in for ``picotron.nn.triton_kernels.cross_entropy`` (reference
+src/picotron/nn/triton_kernels/cross_entropy.py).  The reference kernel is inference-only,
+2-D, vocab <= 65536, without ``ignore_index``, and checks targets with a host sync; its
+callers fall back to ``F.cross_entropy``.  Here ``triton_cross_entropy`` returns the same
+value as ``F.cross_entropy(logits, targets)`` (mean over targets != -100, fp32) and, when
+the logits require grad, writes d(loss)/d(logits) into the logits' storage during the
+forward (one HBM read + one write of the logits in total).  The backward only rescales by
+the incoming gradient, on device, and skips even that when it is exactly 1.
+
+In-place contract: after a grad-enabled call the logits tensor holds the gradient, not
+the logits.  Its autograd version counter is bumped, so any other graph node that saved
+those logits fails loudly at backward instead of reading wrong values.  Pass
+``inplace=False`` to keep the logits (the gradient then goes to a copy).
+"""
+
+from __future__ import annotations
+
+import os
+import warnings
+
+import torch
+from torch import Tensor
+from torch.nn import functional as F
+
+from picotron_amd import ops
+from picotron_amd.nn.triton_kernels._gate import require_hip
+
+IGNORE_INDEX = -100
+_CHECK_ENV = "PICOTRON_HIP_CE_CHECK"
+
+
+class TritonCrossEntropyUnavailable(RuntimeError):
+    """Raised when the fused (HIP) cross-entropy path cannot safely run."""
+
+
+class _FusedCrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits: Tensor, targets: Tensor, ignore_index: int, inplace: bool):  # type: ignore[override]
+        write_grad = ctx.needs_input_grad[0]
+        buffer = logits.detach()
+        if write_grad and not inplace:
+            buffer = buffer.clone()
+        loss, _ = ops.cross_entropy(buffer, targets, ignore_index, write_grad=write_grad)
+        if write_grad:
+            if inplace:
+                torch.autograd.graph.increment_version(logits)
+            ctx.grad_buffer = buffer
+            ctx.targets = targets
+            ctx.ignore_index = ignore_index
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss: Tensor):  # type: ignore[override]
+        grad = ctx.grad_buffer
+        ops.cross_entropy_scale_grad(grad, ctx.targets, grad_loss, ctx.ignore_index)
+        del ctx.grad_buffer
+        return grad, None, None, None
+
+
+def _validate(logits: Tensor, targets: Tensor, ignore_index: int) -> None:
+    require_hip(TritonCrossEntropyUnavailable, "cross-entropy", logits, targets)
+    if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise TritonCrossEntropyUnavailable("HIP cross-entropy supports float logits only.")
+    try:
+        outer, inner, _, _, _ = ops.ce_rows(logits)
+        ops.ce_target_strides(targets, outer, inner)
+    except ValueError as error:
+        raise TritonCrossEntropyUnavailable(f"HIP cross-entropy: {error}.") from error
+    if os.environ.get(_CHECK_ENV, "") not in ("", "0"):
+        vocab = logits.size(1)
+        bad = ((targets < 0) | (targets >= vocab)) & (targets != ignore_index)
+        if bool(bad.any().item()):
+            raise TritonCrossEntropyUnavailable("HIP cross-entropy targets are out of range.")
+
+
+def triton_cross_entropy(
+    logits: Tensor, targets: Tensor, *, ignore_index: int = IGNORE_INDEX, inplace: bool = True
+) -> Tensor:
+    """Mean cross-entropy over targets != ignore_index as an fp32 scalar.
+
+    ``logits`` is (N, C) or (N, C, d) with a contiguous class dimension (such as the
+    ``logits[:, :-1, :].transpose(1, 2)`` view of the train loop); ``targets`` is (N,) or
+    (N, d) int64.  A non-ignored target outside [0, C) gives a NaN loss (set
+    PICOTRON_HIP_CE_CHECK=1 to raise instead, at the cost of a host sync).
+    """
+
+    _validate(logits, targets, ignore_index)
+    return _FusedCrossEntropy.apply(logits, targets, int(ignore_index), bool(inplace))
+
+
+class CrossEntropyWithFallback:
+    """Run the fused cross-entropy when enabled, else (or on failure) ``F.cross_entropy``
+    (reference cross_entropy.py:90-109)."""
+
+    def __init__(self, *, use_triton: bool = False) -> None:
+        self.use_triton = use_triton
+        self._fallback_warned = False
+
+    def __call__(self, logits: Tensor, targets: Tensor) -> Tensor:
+        if self.use_triton:
+            try:
+                return triton_cross_entropy(logits, targets)
+            except Exception as error:
+                if not self._fallback_warned:
+                    warnings.warn(
+                        f"Triton cross-entropy unavailable; using PyTorch fallback: {error}",
+                        RuntimeWarning,
+                        stacklevel=2,
+                    )
+                    self._fallback_warned = True
+        return F.cross_entropy(logits, targets)

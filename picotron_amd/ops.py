@@ -1,0 +1,367 @@
+"""Tensor-level launchers for the HIP kernels: shape/stride checks, output allocation,
+and the ctypes call on the caller's current HIP stream.
+
+These functions never fall back to PyTorch arithmetic: if the library is missing they
+raise :class:`picotron_amd._lib.HipLibraryUnavailable`, and if an entry point rejects its
+arguments they raise :class:`picotron_amd._lib.HipKernelError`.  The autograd Functions
+in :mod:`picotron_amd.nn.triton_kernels` are built on them.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+
+import torch
+from torch import Tensor
+
+from picotron_amd import _lib
+
+_DTYPE_CODES = {
+    torch.float32: _lib.PT_FLOAT32,
+    torch.float16: _lib.PT_FLOAT16,
+    torch.bfloat16: _lib.PT_BFLOAT16,
+}
+
+LAYOUTS = {"interleaved": 0, "rotate_half": 1}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+@functools.lru_cache(maxsize=None)
+def device_supported(index: int) -> bool:
+    """True if CUDA/HIP device ``index`` is a gfx950 GPU the library was built for."""
+
+    return bool(_lib.lib().pt_device_supported(index))
+
+
+def _check_cuda(*tensors: Tensor) -> torch.device:
+    device = tensors[0].device
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("HIP kernels need tensors on a GPU device")
+        if t.device != device:
+            raise ValueError("all tensors must be on the same device")
+    return device
+
+
+# ------------------------------------------------------------------ RMSNorm
+
+
+def _as_rows(t: Tensor, cols: int) -> Tensor:
+    """(rows, cols) view of ``t`` whose last dim is contiguous; copies only if needed."""
+
+    if t.dim() == 2 and t.size(1) == cols and (t.stride(1) == 1 or cols == 1):
+        return t
+    flat = t.reshape(-1, cols)
+    if flat.size(0) > 1 and flat.stride(1) != 1:
+        flat = flat.contiguous()
+    return flat
+
+
+def rmsnorm_fwd(x: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """y = x * rsqrt(mean(x^2) + eps) * weight over the last dim; returns (y, rstd fp32)."""
+
+    device = _check_cuda(x, weight)
+    cols = x.size(-1)
+    if weight.dim() != 1 or weight.numel() != cols:
+        raise ValueError("RMSNorm weight must be 1-D with hidden-size elements")
+    weight = weight.contiguous()
+    x2 = _as_rows(x, cols)
+    rows = x2.size(0)
+    y = torch.empty(x.shape, dtype=x.dtype, device=device)
+    rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=device)
+    y2 = y.view(-1, cols)
+    _lib.call(
+        "pt_rmsnorm_fwd",
+        x2.data_ptr(), x2.stride(0) if rows > 1 else cols, weight.data_ptr(), y2.data_ptr(), cols,
+        rstd.data_ptr(), rows, cols, float(eps), dtype_code(x.dtype), dtype_code(weight.dtype),
+        _stream(device),
+    )
+    return y, rstd
+
+
+def rmsnorm_bwd(
+    dy: Tensor,
+    x: Tensor,
+    weight: Tensor,
+    rstd: Tensor,
+    need_dx: bool = True,
+    need_dw: bool = True,
+) -> tuple[Tensor | None, Tensor | None]:
+    """Gradients of RMSNorm w.r.t. x (x's dtype) and weight (weight's dtype)."""
+
+    device = _check_cuda(dy, x, weight, rstd)
+    cols = x.size(-1)
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    weight = weight.contiguous()
+    rstd = rstd.contiguous()
+    x2 = _as_rows(x, cols)
+    dy2 = _as_rows(dy, cols)
+    rows = x2.size(0)
+    if rstd.numel() != rows or rstd.dtype != torch.float32:
+        raise ValueError("rstd must hold one fp32 value per row")
+    dx = torch.empty(x.shape, dtype=x.dtype, device=device) if need_dx else None
+    dw = torch.empty(cols, dtype=weight.dtype, device=device) if need_dw else None
+    ws = None
+    ws_bytes = 0
+    if need_dw:
+        ws_bytes = _lib.lib().pt_rmsnorm_bwd_workspace_bytes(rows, cols, dtype_code(x.dtype))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
+    if not need_dx and not need_dw:
+        return None, None
+    _lib.call(
+        "pt_rmsnorm_bwd",
+        dy2.data_ptr(), dy2.stride(0) if rows > 1 else cols, x2.data_ptr(),
+        x2.stride(0) if rows > 1 else cols, weight.data_ptr(), rstd.data_ptr(), _ptr(dx), cols,
+        _ptr(dw), _ptr(ws), ws_bytes, rows, cols, dtype_code(x.dtype), dtype_code(weight.dtype),
+        _stream(device),
+    )
+    return dx, dw
+
+
+# ------------------------------------------------------------------ SwiGLU
+
+
+def _flat(t: Tensor) -> Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def swiglu_fwd(gate: Tensor, up: Tensor) -> Tensor:
+    """silu(gate) * up, elementwise, in gate's dtype."""
+
+    device = _check_cuda(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("SwiGLU gate and up must match in shape and dtype")
+    gate, up = _flat(gate), _flat(up)
+    out = torch.empty_like(gate)
+    _lib.call(
+        "pt_swiglu_fwd", gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+        dtype_code(gate.dtype), _stream(device),
+    )
+    return out
+
+
+def swiglu_bwd(
+    dout: Tensor, gate: Tensor, up: Tensor, need_dgate: bool = True, need_dup: bool = True
+) -> tuple[Tensor | None, Tensor | None]:
+    device = _check_cuda(dout, gate, up)
+    if dout.dtype != gate.dtype:
+        dout = dout.to(gate.dtype)
+    dout, gate, up = _flat(dout), _flat(gate), _flat(up)
+    dg = torch.empty_like(gate) if need_dgate else None
+    du = torch.empty_like(up) if need_dup else None
+    _lib.call(
+        "pt_swiglu_bwd", dout.data_ptr(), gate.data_ptr(), up.data_ptr(), _ptr(dg), _ptr(du),
+        gate.numel(), dtype_code(gate.dtype), _stream(device),
+    )
+    return dg, du
+
+
+# ------------------------------------------------------------------ RoPE
+
+
+def _rope_desc(x: Tensor, y: Tensor) -> ctypes.Array:
+    b, h, s, _ = x.shape
+    return (ctypes.c_int64 * 9)(
+        b, h, s, x.stride(0), x.stride(1), x.stride(2), y.stride(0), y.stride(1), y.stride(2)
+    )
+
+
+def rope(
+    x0: Tensor,
+    cos: Tensor,
+    sin: Tensor,
+    *,
+    layout: str = "interleaved",
+    inverse: bool = False,
+    x1: Tensor | None = None,
+) -> tuple[Tensor, Tensor | None]:
+    """Rotate (batch, heads, seq, head_dim) views x0 (and x1) by the angle tables.
+
+    ``cos``/``sin`` are fp32 ``[>= seq, head_dim/2]`` tables; row ``s`` is position ``s``.
+    Outputs are new tensors with the inputs' logical shape and memory layout.
+    """
+
+    device = _check_cuda(x0, cos, sin) if x1 is None else _check_cuda(x0, x1, cos, sin)
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(LAYOUTS)}")
+    tensors = [x0] if x1 is None else [x0, x1]
+    head_dim = x0.size(-1)
+    for t in tensors:
+        if t.dim() != 4 or t.size(-1) != head_dim or t.stride(-1) != 1:
+            raise ValueError("RoPE states must be 4-D (batch, heads, seq, head_dim), head_dim contiguous")
+        if t.dtype != x0.dtype:
+            raise ValueError("query and key must share a dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("RoPE tables must be fp32")
+    cos = cos.contiguous()
+    sin = sin.contiguous()
+    if cos.dim() != 2 or cos.shape != sin.shape or cos.size(1) * 2 != head_dim:
+        raise ValueError("RoPE tables must be [seq, head_dim/2]")
+    # empty_like keeps the input's stride order (dense inputs), so a (B,S,H,D)-memory view
+    # comes back with the same memory layout.
+    outs = [torch.empty_like(t) for t in tensors]
+    descs = [_rope_desc(t, o) for t, o in zip(tensors, outs)]
+    _lib.call(
+        "pt_rope",
+        x0.data_ptr(), outs[0].data_ptr(), descs[0],
+        None if x1 is None else x1.data_ptr(), None if x1 is None else outs[1].data_ptr(),
+        None if x1 is None else descs[1],
+        head_dim, cos.data_ptr(), sin.data_ptr(), cos.size(0), LAYOUTS[layout], int(inverse),
+        dtype_code(x0.dtype), _stream(device),
+    )
+    return outs[0], (outs[1] if x1 is not None else None)
+
+
+# ------------------------------------------------------------------ cross-entropy
+
+
+def ce_rows(logits: Tensor) -> tuple[int, int, int, int, int]:
+    """(outer, inner, outer_stride, inner_stride, vocab) of a (N, V) or (B, V, S) input
+    whose class dimension (dim 1) is contiguous."""
+
+    if logits.dim() == 2:
+        n, v = logits.shape
+        if logits.stride(1) != 1 and v > 1:
+            raise ValueError("cross-entropy logits need a contiguous class dimension")
+        return n, 1, logits.stride(0), 0, v
+    if logits.dim() == 3:
+        b, v, s = logits.shape
+        if logits.stride(1) != 1 and v > 1:
+            raise ValueError("cross-entropy logits need a contiguous class dimension")
+        return b, s, logits.stride(0), logits.stride(2), v
+    raise ValueError("cross-entropy logits must be (N, C) or (N, C, d)")
+
+
+def ce_target_strides(targets: Tensor, outer: int, inner: int) -> tuple[int, int]:
+    if targets.dtype != torch.long:
+        raise ValueError("cross-entropy targets must be int64")
+    if targets.dim() == 1 and inner == 1:
+        if targets.numel() != outer:
+            raise ValueError("targets must have one entry per row")
+        return targets.stride(0), 0
+    if targets.dim() == 2 and tuple(targets.shape) == (outer, inner):
+        return targets.stride(0), targets.stride(1)
+    raise ValueError("targets shape does not match the logits")
+
+
+def cross_entropy(
+    logits: Tensor, targets: Tensor, ignore_index: int = -100, write_grad: bool = False
+) -> tuple[Tensor, Tensor]:
+    """Mean cross-entropy (fp32 scalar tensor) over targets != ignore_index.
+
+    With ``write_grad`` the logits are overwritten in place by d(loss)/d(logits).
+    Returns (loss, workspace); the workspace holds the status word (bit 0: a target out
+    of range), readable with :func:`cross_entropy_status`.
+    """
+
+    device = _check_cuda(logits, targets)
+    outer, inner, os_, is_, vocab = ce_rows(logits)
+    tos, tis = ce_target_strides(targets, outer, inner)
+    rows = outer * inner
+    ws_bytes = _lib.lib().pt_cross_entropy_workspace_bytes(rows)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    loss = torch.empty((), dtype=torch.float32, device=device)
+    _lib.call(
+        "pt_cross_entropy",
+        logits.data_ptr(), outer, inner, os_, is_, vocab, targets.data_ptr(), tos, tis,
+        int(ignore_index), loss.data_ptr(), int(write_grad), ws.data_ptr(), ws_bytes,
+        dtype_code(logits.dtype), _stream(device),
+    )
+    return loss, ws
+
+
+def cross_entropy_status(ws: Tensor) -> int:
+    """Status word of a cross-entropy workspace (synchronises with the device)."""
+
+    return int(ws[8:12].view(torch.int32).item())
+
+
+def cross_entropy_scale_grad(
+    dlogits: Tensor, targets: Tensor, grad_output: Tensor, ignore_index: int = -100
+) -> None:
+    """dlogits *= grad_output in place (skipped on device when grad_output == 1)."""
+
+    device = _check_cuda(dlogits, targets, grad_output)
+    outer, inner, os_, is_, vocab = ce_rows(dlogits)
+    tos, tis = ce_target_strides(targets, outer, inner)
+    go = grad_output.detach().to(torch.float32).reshape(())
+    _lib.call(
+        "pt_cross_entropy_scale_grad",
+        dlogits.data_ptr(), outer, inner, os_, is_, vocab, targets.data_ptr(), tos, tis,
+        int(ignore_index), go.data_ptr(), dtype_code(dlogits.dtype), _stream(device),
+    )
+
+
+# ------------------------------------------------------------------ AdamW
+
+
+def adamw_block_elems() -> int:
+    return int(_lib.lib().pt_adamw_block_elems())
+
+
+def adamw_table(
+    params: list[Tensor], grads: list[Tensor], exp_avgs: list[Tensor], exp_avg_sqs: list[Tensor]
+) -> tuple[Tensor, int]:
+    """Host int64 [n, 6] table for :func:`adamw_step` and its total block count."""
+
+    per = adamw_block_elems()
+    rows = []
+    first = 0
+    for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs):
+        n = p.numel()
+        if n == 0:
+            continue
+        rows.append([p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), n, first])
+        first += (n + per - 1) // per
+    table = torch.tensor(rows, dtype=torch.int64) if rows else torch.empty((0, 6), dtype=torch.int64)
+    return table, first
+
+
+def adamw_step(
+    table_device: Tensor,
+    total_blocks: int,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: float,
+) -> None:
+    """One AdamW step over the tensors in a device table built from :func:`adamw_table`."""
+
+    device = _check_cuda(table_device)
+    _lib.call(
+        "pt_adamw_step",
+        table_device.data_ptr(), table_device.size(0), int(total_blocks), float(lr), float(beta1),
+        float(beta2), float(eps), float(weight_decay), float(step), _stream(device),
+    )
+
+
+# ------------------------------------------------------------------ utility
+
+
+def copy_bytes(src: Tensor, dst: Tensor) -> None:
+    """128-bit streaming device copy of src into dst (same byte size)."""
+
+    device = _check_cuda(src, dst)
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes or not src.is_contiguous() or not dst.is_contiguous():
+        raise ValueError("copy_bytes needs contiguous tensors of equal byte size")
+    _lib.call("pt_copy", src.data_ptr(), dst.data_ptr(), nbytes, _stream(device))

@@ -1,0 +1,82 @@
+"""The C-ABI library loads, exports every entry point include/picotron_hip.h declares, and
+its host-side queries and argument validation behave.  No kernel launches (CPU only)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+from picotron_amd import _lib
+
+HEADER = ROOT / "include" / "picotron_hip.h"
+
+
+def _declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_loads_with_matching_abi_version():
+    lib = _lib.lib()
+    assert lib.pt_abi_version() == _lib.ABI_VERSION
+    header_version = re.search(r"#define PT_ABI_VERSION (\d+)", HEADER.read_text()).group(1)
+    assert int(header_version) == _lib.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = _declared_functions()
+    assert len(declared) >= 16
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in sorted(declared):
+        assert hasattr(raw, name), f"{name} declared in the header but not exported"
+    assert declared == set(_lib.SIGNATURES), "ctypes signature table differs from the header"
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    for name in ("PT_FLOAT32", "PT_FLOAT16", "PT_BFLOAT16", "PT_OK", "PT_EINVAL",
+                 "PT_EUNSUPPORTED", "PT_ELAUNCH", "PT_EDEVICE"):
+        value = int(re.search(rf"#define {name} (\d+)", text).group(1))
+        assert getattr(_lib, name) == value
+
+
+def test_workspace_queries():
+    lib = _lib.lib()
+    # RMSNorm backward at 16384 x 4096: 512 partial rows of 4096 fp32
+    assert lib.pt_rmsnorm_bwd_workspace_bytes(16384, 4096, _lib.PT_BFLOAT16) == 512 * 4096 * 4
+    assert lib.pt_rmsnorm_bwd_workspace_bytes(3, 128, _lib.PT_FLOAT32) == 1 * 128 * 4
+    assert lib.pt_rmsnorm_bwd_workspace_bytes(0, 128, _lib.PT_FLOAT32) == 0
+    assert lib.pt_cross_entropy_workspace_bytes(8192) == 16 + 8192 * 4
+    assert lib.pt_adamw_block_elems() == 4096
+
+
+@pytest.mark.parametrize(
+    "fn,args,code",
+    [
+        ("pt_rmsnorm_fwd", (None, 0, None, None, 0, None, 4, 8, 1e-6, 0, 0, None), _lib.PT_EINVAL),
+        ("pt_rmsnorm_fwd", (None, 0, None, None, 0, None, 4, 8, 1e-6, 7, 0, None), _lib.PT_EINVAL),
+        ("pt_rmsnorm_fwd", (None, 0, None, None, 0, None, 4, 1 << 22, 1e-6, 0, 0, None), _lib.PT_EUNSUPPORTED),
+        ("pt_swiglu_fwd", (None, None, None, -1, 2, None), _lib.PT_EINVAL),
+        ("pt_rope", (None, None, None, None, None, None, 7, None, None, 1, 0, 0, 2, None), _lib.PT_EINVAL),
+        ("pt_adamw_step", (None, 1, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
+        ("pt_copy", (None, None, 16, None), _lib.PT_EINVAL),
+    ],
+)
+def test_invalid_arguments_rejected_before_launch(fn, args, code):
+    rc = getattr(_lib.lib(), fn)(*args)
+    assert rc == code
+    message = _lib.lib().pt_last_error().decode()
+    assert message.startswith(fn)
+    with pytest.raises(_lib.HipKernelError, match=fn):
+        _lib.check(fn, rc)
+
+
+def test_empty_inputs_are_no_ops():
+    lib = _lib.lib()
+    assert lib.pt_swiglu_fwd(None, None, None, 0, 2, None) == _lib.PT_OK
+    assert lib.pt_swiglu_bwd(None, None, None, None, None, 5, 2, None) == _lib.PT_OK
+    assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
+    assert lib.pt_last_error() == b""

@@ -1,0 +1,108 @@
+"""Fused AdamW parity of the HIP kernel (through the C ABI) with the oracle and torch."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from gpu_util import close_fp32, from_npz, randn
+from oracle import adamw as o_adamw
+from picotron_amd import ops
+from picotron_amd.nn.triton_kernels import AdamWStepWithFallback, triton_adamw_step
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+def test_reference_known_answer(gpu):
+    p = torch.nn.Parameter(torch.tensor([1.0], device=gpu))
+    opt = torch.optim.AdamW([p], lr=0.1, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    p.grad = torch.tensor([1.0], device=gpu)
+    triton_adamw_step(opt)
+    assert abs(p.item() - 0.899) < 1e-6
+    assert float(opt.state[p]["step"]) == 1.0
+
+
+def test_golden_fixture(gpu):
+    f = np.load(GOLDEN / "adamw_small.npz")
+    sizes = [int(n) for n in f["sizes"]]
+    params = [torch.nn.Parameter(from_npz(f[f"p0_{i}"], gpu)) for i in range(len(sizes))]
+    opt = torch.optim.AdamW(params, **HP)
+    for t in range(1, int(f["steps"]) + 1):
+        for i, p in enumerate(params):
+            p.grad = from_npz(f[f"g{t}_{i}"], gpu)
+        triton_adamw_step(opt)
+    for i, p in enumerate(params):
+        close_fp32(p.detach(), from_npz(f[f"p_{i}"], gpu))
+        close_fp32(opt.state[p]["exp_avg"], from_npz(f[f"m_{i}"], gpu))
+        close_fp32(opt.state[p]["exp_avg_sq"], from_npz(f[f"v_{i}"], gpu))
+
+
+def test_matches_torch_adamw_multi_tensor(gpu):
+    sizes = [1, 3, 4095, 4096, 4097, 70_000, 1 << 20]
+    fused = [torch.nn.Parameter(randn((n,), torch.float32, gpu, n, 0.02)) for n in sizes]
+    fused.append(torch.nn.Parameter(randn((33, 65), torch.float32, gpu, 5, 0.02)))
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in fused]
+    opt_f = torch.optim.AdamW(fused, **HP)
+    opt_r = torch.optim.AdamW(ref, foreach=False, **HP)
+    for step in range(4):
+        for i, (a, b) in enumerate(zip(fused, ref)):
+            g = randn(a.shape, torch.float32, gpu, 100 * step + i, 1e-3)
+            a.grad, b.grad = g, g.clone()
+        for group in (opt_f.param_groups[0], opt_r.param_groups[0]):
+            group["lr"] = 3e-4 * (1 + step)  # the train loop rewrites lr every step
+        triton_adamw_step(opt_f)
+        opt_r.step()
+    for a, b in zip(fused, ref):
+        close_fp32(a.detach(), b.detach())
+        close_fp32(opt_f.state[a]["exp_avg"], opt_r.state[b]["exp_avg"])
+        close_fp32(opt_f.state[a]["exp_avg_sq"], opt_r.state[b]["exp_avg_sq"])
+    # the state dict has torch's layout and loads into a torch AdamW
+    sd = opt_f.state_dict()
+    opt_r.load_state_dict(sd)
+    assert set(sd["state"][0]) == {"step", "exp_avg", "exp_avg_sq"}
+    assert sd["state"][0]["step"].device.type == "cpu" and float(sd["state"][0]["step"]) == 4.0
+
+
+def test_unaligned_views_and_missing_grads(gpu):
+    flat = randn((10_001,), torch.float32, gpu, 9, 0.02)
+    params = [torch.nn.Parameter(flat[1:5000].clone()), torch.nn.Parameter(flat[:7].clone())]
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    opt_f = torch.optim.AdamW(params, **HP)
+    opt_r = torch.optim.AdamW(ref, foreach=False, **HP)
+    g = randn((6000,), torch.float32, gpu, 10, 1e-3)
+    params[0].grad, ref[0].grad = g[1:5000], g[1:5000].clone()  # 4-byte-offset gradient
+    triton_adamw_step(opt_f)
+    opt_r.step()
+    close_fp32(params[0].detach(), ref[0].detach())
+    assert torch.equal(params[1].detach(), ref[1].detach())  # no grad: untouched
+    assert len(opt_f.state[params[1]]) == 0
+
+
+def test_full_config(gpu):
+    # one step over 1.2e9 fp32 params ~ N(0, 0.02^2), grads ~ N(0, 1e-3^2), at step 2
+    n = 1_200_000_000
+    p = torch.nn.Parameter(randn((n,), torch.float32, gpu, 91, 0.02))
+    opt = torch.optim.AdamW([p], **HP)
+    p.grad = randn((n,), torch.float32, gpu, 92, 1e-3)
+    step = AdamWStepWithFallback(use_triton=True)
+    step.step(opt)  # step 1 creates the state
+    m1 = opt.state[p]["exp_avg"].clone()
+    v1 = opt.state[p]["exp_avg_sq"].clone()
+    p1 = p.detach().clone()
+    p.grad = randn((n,), torch.float32, gpu, 93, 1e-3)
+    step.step(opt)
+    assert not step._fallback_warned
+    # fp32 oracle evaluated by torch on the GPU, in slices (memory)
+    for lo in range(0, n, 200_000_000):
+        hi = min(n, lo + 200_000_000)
+        ep, em, ev = o_adamw.step(
+            p1[lo:hi], p.grad[lo:hi], m1[lo:hi], v1[lo:hi], t=2, lr=3e-4, beta1=0.9, beta2=0.95,
+            eps=1e-8, weight_decay=0.1, compute=torch.float32,
+        )
+        close_fp32(p.detach()[lo:hi], ep)
+        close_fp32(opt.state[p]["exp_avg"][lo:hi], em)
+        close_fp32(opt.state[p]["exp_avg_sq"][lo:hi], ev)

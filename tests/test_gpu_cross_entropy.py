@@ -1,0 +1,152 @@
+"""Fused cross-entropy parity of the HIP kernels (through the C ABI) with the oracle."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from gpu_util import from_npz, randn
+from oracle import cross_entropy as o_ce
+from picotron_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+LOSS_RTOL = 1e-4  # fp32-accumulated loss vs the fp64 oracle
+
+
+def _grad_close(grad, ref, n_valid, dtype):
+    # d loss/d logits = (softmax - onehot) / n_valid: compare (softmax - onehot) so the
+    # relative tolerance of the storage type applies to O(1/V)..O(1) values.
+    rtol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
+    torch.testing.assert_close(
+        grad.double() * n_valid, ref.double() * n_valid, rtol=rtol, atol=1e-9 if dtype == torch.float32 else 1e-7
+    )
+
+
+def _check(logits, targets, dtype):
+    ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
+    n_valid = int((targets != -100).sum())
+    loss, ws = ops.cross_entropy(logits, targets)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    buf = logits.clone()
+    loss2, ws = ops.cross_entropy(buf, targets, write_grad=True)
+    assert loss2.item() == loss.item()  # the loss does not depend on writing the gradient
+    assert ops.cross_entropy_status(ws) == 0
+    _grad_close(buf, ref_grad, n_valid, dtype)
+    return buf
+
+
+def test_reference_known_answer(gpu):
+    f = np.load(GOLDEN / "cross_entropy_reference_kat.npz")
+    logits = from_npz(f["logits"], gpu)
+    targets = from_npz(f["targets"], gpu)
+    loss, _ = ops.cross_entropy(logits, targets)
+    assert abs(loss.item() - 1.2887259920) < 1e-6
+    buf = logits.clone()
+    ops.cross_entropy(buf, targets, write_grad=True)
+    torch.testing.assert_close(buf, from_npz(f["grad"], gpu), rtol=1e-5, atol=1e-7)
+
+
+def test_golden_fixture(gpu):
+    f = np.load(GOLDEN / "cross_entropy_small.npz")
+    logits = from_npz(f["logits"], gpu)
+    targets = from_npz(f["targets"], gpu)
+    loss, _ = ops.cross_entropy(logits, targets)
+    assert abs(loss.item() - float(f["loss"])) <= 1e-5 * abs(float(f["loss"]))
+    buf = logits.clone()
+    ops.cross_entropy(buf, targets, write_grad=True)
+    _grad_close(buf, from_npz(f["grad"], gpu), 13, torch.float32)
+
+
+def test_full_config_bf16(gpu):
+    # logits [8192, 128256] bf16 ~ N(0, 2^2); targets uniform, exactly 410 (5%) ignored
+    rows, vocab = 8192, 128256
+    logits = randn((rows, vocab), torch.bfloat16, gpu, 51, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(52)
+    targets = torch.randint(0, vocab, (rows,), generator=g, device=gpu)
+    targets[torch.randperm(rows, generator=g, device=gpu)[:410]] = -100
+    ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
+    loss, ws = ops.cross_entropy(logits, targets, write_grad=True)  # in place
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    assert ops.cross_entropy_status(ws) == 0
+    _grad_close(logits, ref_grad, rows - 410, torch.bfloat16)
+    # size-independent: every kept row of (softmax - onehot) sums to 0, ignored rows are 0
+    row_sums = logits.double().sum(-1) * (rows - 410)
+    assert float(row_sums.abs().max()) < 5e-3
+    assert bool((logits[targets == -100] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,vocab", [(1, 1), (5, 3), (7, 1000), (33, 8192), (4, 50257), (3, 131072), (2, 262144)])
+def test_shapes(gpu, dtype, rows, vocab):
+    logits = randn((rows, vocab), dtype, gpu, rows * 3 + vocab, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(vocab)
+    targets = torch.randint(0, vocab, (rows,), generator=g, device=gpu)
+    if rows > 2:
+        targets[1] = -100
+    _check(logits, targets, dtype)
+
+
+def test_train_loop_view(gpu):
+    # loss(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:]) on (B, S, V) bf16 logits
+    b, s, v = 2, 65, 3000
+    full = randn((b, s, v), torch.bfloat16, gpu, 61, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(62)
+    ids = torch.randint(0, v, (b, s), generator=g, device=gpu)
+    view = full[:, :-1, :].transpose(1, 2)
+    targets = ids[:, 1:]
+    ref_loss, ref_grad = o_ce.forward_backward(view, targets)
+    last = full[:, -1, :].clone()
+    loss, _ = ops.cross_entropy(view, targets, write_grad=True)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    _grad_close(view, ref_grad, b * (s - 1), torch.bfloat16)
+    assert torch.equal(full[:, -1, :], last)  # the unused last position is untouched
+
+
+def test_ignored_rows_and_bad_targets(gpu):
+    logits = randn((6, 100), torch.float32, gpu, 71)
+    targets = torch.full((6,), -100, device=gpu)
+    buf = logits.clone()
+    loss, _ = ops.cross_entropy(buf, targets, write_grad=True)
+    assert math.isnan(loss.item())  # 0 / 0, as F.cross_entropy
+    assert bool((buf == 0).all())
+    bad = torch.tensor([1, 100, 3, -5, 2, 0], device=gpu)
+    loss, ws = ops.cross_entropy(logits, bad)
+    assert math.isnan(loss.item()) and ops.cross_entropy_status(ws) & 1
+
+
+def test_autograd_surface_and_grad_scaling(gpu):
+    import warnings
+
+    from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback, triton_cross_entropy
+
+    full = randn((2, 33, 500), torch.bfloat16, gpu, 81, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(82)
+    ids = torch.randint(0, 500, (2, 33), generator=g, device=gpu)
+    ids[0, 5] = -100
+    ref_loss, ref_grad = o_ce.forward_backward(full[:, :-1, :].transpose(1, 2), ids[:, 1:])
+    leaf = full.clone().requires_grad_(True)
+    logits = leaf * 1  # non-leaf, as a projection output
+    ce = CrossEntropyWithFallback(use_triton=True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        loss = ce(logits[:, :-1, :].transpose(1, 2), ids[:, 1:])
+    assert not ce._fallback_warned
+    assert loss.dtype == torch.float32
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    (3.0 * loss).backward()  # grad_output != 1 takes the on-device scaling path
+    n_valid = int((ids[:, 1:] != -100).sum())
+    expected = torch.zeros_like(full, dtype=torch.float64)
+    expected[:, :-1, :] = 3.0 * ref_grad.transpose(1, 2)
+    _grad_close(leaf.grad, expected, n_valid, torch.bfloat16)
+    # inplace=False keeps the logits intact
+    x = full.clone().requires_grad_(True)
+    y = x * 1
+    loss2 = triton_cross_entropy(y[:, :-1, :].transpose(1, 2), ids[:, 1:], inplace=False)
+    assert torch.equal(y.detach(), full)
+    loss2.backward()
+    _grad_close(x.grad, expected / 3.0, n_valid, torch.bfloat16)

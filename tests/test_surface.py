@@ -1,0 +1,200 @@
+"""The reference's hot-path tests, run against this package's drop-in surface on CPU
+(reference tests/test_triton_{rmsnorm_backward,swiglu_backward,rmsnorm_swiglu_rope,kernels,
+ce_adamw}.py and tests/test_rope.py).  On CPU every fused path must raise its
+``*Unavailable`` exception and the modules must warn once and fall back."""
+
+from __future__ import annotations
+
+import warnings
+
+import pytest
+import torch
+from torch.nn import functional as F
+from torch.optim import AdamW
+
+from picotron_amd.config import ConfigValidationError, TritonKernelsConfig
+from picotron_amd.hardware import detect_triton_support
+from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU, apply_rotary_embedding, rotary_cos_sin
+from picotron_amd.nn.rope import apply_rotary_embedding_rotate_half
+from picotron_amd.nn.triton_kernels import (
+    AdamWStepWithFallback,
+    CrossEntropyWithFallback,
+    TritonAdamWUnavailable,
+    TritonAttentionUnavailable,
+    TritonCrossEntropyUnavailable,
+    TritonRMSNormUnavailable,
+    TritonRoPEUnavailable,
+    TritonSwiGLUUnavailable,
+    rms_norm_with_pytorch_forward,
+    swiglu_with_pytorch_forward,
+    triton_adamw_step,
+    triton_apply_rotary_embedding,
+    triton_causal_attention,
+    triton_cross_entropy,
+    triton_rms_norm,
+    triton_swiglu,
+)
+
+
+def test_public_names_match_reference_all():
+    import picotron_amd.nn.triton_kernels as tk
+
+    reference_all = {
+        "AdamWStepWithFallback", "CrossEntropyWithFallback", "TritonAttentionUnavailable",
+        "TritonAdamWUnavailable", "TritonCrossEntropyUnavailable", "TritonRMSNormUnavailable",
+        "TritonRoPEUnavailable", "TritonSwiGLUUnavailable", "triton_causal_attention",
+        "triton_apply_rotary_embedding", "triton_cross_entropy", "triton_rms_norm",
+        "triton_swiglu", "swiglu_with_pytorch_forward", "rms_norm_with_pytorch_forward",
+    }
+    assert reference_all <= set(tk.__all__)
+    for exc in (TritonAdamWUnavailable, TritonAttentionUnavailable, TritonCrossEntropyUnavailable,
+                TritonRMSNormUnavailable, TritonRoPEUnavailable, TritonSwiGLUUnavailable):
+        assert issubclass(exc, RuntimeError)
+
+
+def test_custom_rmsnorm_backward_matches_native_rmsnorm():
+    torch.manual_seed(23)
+    eps = 1e-6
+    upstream = torch.randn(2, 3, 8, dtype=torch.float32)
+    x = torch.randn(2, 3, 8, dtype=torch.float32, requires_grad=True)
+    w = torch.randn(8, dtype=torch.float32, requires_grad=True)
+    out = rms_norm_with_pytorch_forward(x, w, eps)
+    (out * upstream).sum().backward()
+    xn = x.detach().clone().requires_grad_(True)
+    wn = w.detach().clone().requires_grad_(True)
+    native = xn * torch.rsqrt(xn.square().mean(dim=-1, keepdim=True) + eps) * wn
+    (native * upstream).sum().backward()
+    torch.testing.assert_close(out, native, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(x.grad, xn.grad, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(w.grad, wn.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_custom_swiglu_backward_matches_native_pytorch():
+    torch.manual_seed(31)
+    upstream = torch.randn(2, 3, 7, dtype=torch.float64)
+    g = torch.randn(2, 3, 7, dtype=torch.float64, requires_grad=True)
+    u = torch.randn(2, 3, 7, dtype=torch.float64, requires_grad=True)
+    out = swiglu_with_pytorch_forward(g, u)
+    (out * upstream).sum().backward()
+    gn = g.detach().clone().requires_grad_(True)
+    un = u.detach().clone().requires_grad_(True)
+    (F.silu(gn) * un * upstream).sum().backward()
+    torch.testing.assert_close(out, F.silu(gn) * un, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(g.grad, gn.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(u.grad, un.grad, rtol=1e-10, atol=1e-10)
+
+
+def test_fused_entry_points_raise_unavailable_on_cpu():
+    x = torch.randn(2, 3, 8)
+    with pytest.raises(TritonRMSNormUnavailable):
+        triton_rms_norm(x, torch.ones(8), 1e-6)
+    with pytest.raises(TritonSwiGLUUnavailable):
+        triton_swiglu(x, x)
+    cos, sin = rotary_cos_sin(3, 8, 1e4, device=x.device, dtype=torch.float32)
+    with pytest.raises(TritonRoPEUnavailable):
+        triton_apply_rotary_embedding(torch.randn(2, 4, 3, 8), cos, sin)
+    with pytest.raises(TritonCrossEntropyUnavailable):
+        triton_cross_entropy(torch.randn(4, 5), torch.tensor([0, 1, 2, 3]))
+    with pytest.raises(TritonAttentionUnavailable):
+        triton_causal_attention(x, x, x)
+
+
+def test_triton_enabled_cpu_fallbacks_match_native_pytorch():
+    hidden = torch.randn(2, 3, 8)
+    norm = RMSNorm(8, use_triton_rmsnorm=True)
+    with pytest.warns(RuntimeWarning, match="Triton RMSNorm unavailable"):
+        normalized = norm(hidden)
+    expected = hidden * torch.rsqrt(hidden.pow(2).mean(dim=-1, keepdim=True) + norm.eps)
+    torch.testing.assert_close(normalized, expected * norm.weight)
+    assert norm._triton_fallback_warned
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # warn once only
+        norm(hidden)
+
+    swiglu = SwiGLU(8, 16, use_triton_swiglu=True)
+    with pytest.warns(RuntimeWarning, match="Triton SwiGLU unavailable"):
+        fused = swiglu(hidden)
+    expected_swiglu = swiglu.down_projection(
+        F.silu(swiglu.gate_projection(hidden)) * swiglu.up_projection(hidden)
+    )
+    torch.testing.assert_close(fused, expected_swiglu)
+
+    query = torch.randn(2, 4, 3, 8)
+    key = torch.randn(2, 4, 3, 8)
+    fast = RotaryEmbedding(8, use_triton_rope=True)
+    native = RotaryEmbedding(8)
+    with pytest.warns(RuntimeWarning, match="Triton RoPE unavailable"):
+        fq, fk = fast(query, key)
+    nq, nk = native(query, key)
+    torch.testing.assert_close(fq, nq)
+    torch.testing.assert_close(fk, nk)
+
+
+def test_rope_dot_product_depends_only_on_relative_position():
+    torch.manual_seed(0)
+    d = 8
+    q = torch.randn(1, 1, 1, d).expand(-1, -1, 12, -1).clone()
+    k = torch.randn(1, 1, 1, d).expand(-1, -1, 12, -1).clone()
+    cos, sin = rotary_cos_sin(12, d, 10_000.0, device=q.device, dtype=q.dtype)
+    for apply in (apply_rotary_embedding, apply_rotary_embedding_rotate_half):
+        rq, rk = apply(q, cos, sin), apply(k, cos, sin)
+        torch.testing.assert_close((rq[:, :, 2] * rk[:, :, 5]).sum(), (rq[:, :, 6] * rk[:, :, 9]).sum())
+
+
+def test_rotary_embedding_validates_like_reference():
+    with pytest.raises(ValueError):
+        RotaryEmbedding(7)
+    with pytest.raises(ValueError):
+        RotaryEmbedding(8, theta=0)
+    with pytest.raises(ValueError):
+        RotaryEmbedding(8)(torch.randn(2, 4, 3, 8), torch.randn(2, 4, 5, 8))
+
+
+def test_triton_cross_entropy_cpu_fallback_matches_pytorch():
+    logits = torch.tensor([[2.0, 0.0, -1.0], [0.5, 1.5, -0.5]])
+    targets = torch.tensor([0, 2], dtype=torch.long)
+    ce = CrossEntropyWithFallback(use_triton=True)
+    with pytest.warns(RuntimeWarning, match="Triton cross-entropy unavailable"):
+        actual = ce(logits, targets)
+    torch.testing.assert_close(actual, F.cross_entropy(logits, targets))
+    assert abs(actual.item() - 1.2887259920) < 1e-6
+    assert callable(triton_cross_entropy)
+
+
+def test_adamw_fallback_matches_known_single_step_update():
+    parameter = torch.nn.Parameter(torch.tensor([1.0]))
+    optimizer = AdamW([parameter], lr=0.1, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    parameter.grad = torch.tensor([1.0])
+    step = AdamWStepWithFallback(use_triton=True)
+    with pytest.warns(RuntimeWarning, match="Triton AdamW unavailable"):
+        step.step(optimizer)
+    torch.testing.assert_close(parameter.detach(), torch.tensor([0.899]))
+    with pytest.raises(RuntimeError, match="not implemented"):
+        triton_adamw_step(optimizer)
+    # the fallback left torch's own state untouched by the fused path
+    assert float(optimizer.state[parameter]["step"]) == 1.0
+
+
+def test_detect_triton_support_on_cpu():
+    report = detect_triton_support()
+    assert not report.enabled and not report.available and not report.hardware_compatible
+    assert not detect_triton_support(enabled=True).available
+
+
+def test_kernel_flags_are_strict_bools():
+    cfg = TritonKernelsConfig(rmsnorm=True, swiglu=True)
+    assert cfg.rmsnorm and cfg.swiglu and not cfg.rope and not cfg.adamw
+    with pytest.raises(ConfigValidationError):
+        TritonKernelsConfig(rmsnorm=1)  # type: ignore[arg-type]
+    with pytest.raises(ConfigValidationError):
+        TritonKernelsConfig.from_mapping({"rmsnorm": True, "layernorm": True})
+    assert TritonKernelsConfig.from_mapping({"cross_entropy": True}).cross_entropy
+
+
+def test_oracle_not_imported_by_product():
+    import pathlib
+    import re
+
+    pkg = pathlib.Path(__file__).resolve().parents[1] / "picotron_amd"
+    for path in pkg.rglob("*.py"):
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", path.read_text(), flags=re.M), path
