@@ -69,6 +69,36 @@ __global__ __launch_bounds__(256) void copy16_kernel(const u32x4* __restrict__ s
   }
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* __restrict__ p, int64_t n,
+                                                        unsigned value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    p[i] = value;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_u16_kernel(unsigned short* __restrict__ p, int64_t n,
+                                                        unsigned short value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    p[i] = value;
+  }
+}
+
+int fill(void* p, int64_t count, int elem_bytes, unsigned value, hipStream_t st) {
+  if (count <= 0) return PT_OK;
+  int64_t blocks = (count + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (elem_bytes == 4) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                       static_cast<unsigned*>(p), count, value);
+  } else {
+    hipLaunchKernelGGL(fill_u16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                       static_cast<unsigned short*>(p), count, static_cast<unsigned short>(value));
+  }
+  return check_launch("fill");
+}
+
 }  // namespace pt
 
 extern "C" {

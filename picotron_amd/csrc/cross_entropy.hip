@@ -65,7 +65,8 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
                                                                int64_t inner, int64_t tos,
                                                                int64_t tis, int64_t rows,
                                                                int64_t ignore_index,
-                                                               CeWork* __restrict__ ws) {
+                                                               CeWork* __restrict__ ws,
+                                                               float* __restrict__ loss_out) {
   __shared__ float red[kWaves];
   float cnt = 0.0f;
   for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
     ws->n_valid = total;
     ws->ticket = 0u;
     ws->status = 0;
+    if (rows == 0) *loss_out = NAN;  // mean over an empty batch: 0/0, as torch returns
   }
 }
 
@@ -397,23 +399,17 @@ int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_s
   // One 1024-thread workgroup per row; an HSA grid holds at most 2^32 - 1 work-items.
   if (rows * kThreads > 0xffffffffLL)
     return fail(PT_EUNSUPPORTED, "pt_cross_entropy: more than 4194303 rows");
-  if (!logits || !targets || !loss_out || !workspace)
-    return fail(PT_EINVAL, "pt_cross_entropy: null pointer");
+  if (!loss_out || !workspace) return fail(PT_EINVAL, "pt_cross_entropy: null pointer");
+  if (rows > 0 && (!logits || !targets)) return fail(PT_EINVAL, "pt_cross_entropy: null pointer");
   if (workspace_bytes < pt_cross_entropy_workspace_bytes(rows) || !aligned16(workspace))
     return fail(PT_EINVAL, "pt_cross_entropy: workspace too small or not 16-byte aligned");
   hipStream_t st = as_stream(stream);
   CeWork* ws = static_cast<CeWork*>(workspace);
   const int64_t inner_nz = inner > 0 ? inner : 1;
   hipLaunchKernelGGL(ce_prepare_kernel, dim3(1), dim3(kThreads), 0, st, targets, inner_nz,
-                     t_outer_stride, t_inner_stride, rows, ignore_index, ws);
+                     t_outer_stride, t_inner_stride, rows, ignore_index, ws, loss_out);
   if (int rc = check_launch("pt_cross_entropy (prepare)")) return rc;
-  if (rows == 0) {
-    // Mean over an empty batch: 0/0, as torch returns.
-    const float nan = NAN;
-    if (hipMemcpyAsync(loss_out, &nan, sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess)
-      return fail(PT_EDEVICE, "pt_cross_entropy: hipMemcpyAsync failed");
-    return ok();
-  }
+  if (rows == 0) return ok();
   const int esize = dtype_size(dtype);
   const bool aligned = aligned16(logits) && (vocab * esize) % 16 == 0 &&
                        (outer <= 1 || (outer_stride * esize) % 16 == 0) &&

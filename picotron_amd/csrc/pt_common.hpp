@@ -25,6 +25,9 @@ int ok();
 int check_launch(const char* what);
 // Number of compute units of the current device (cached per device).
 int num_cus();
+// Fills `count` elements of 4 or 2 bytes at device address `p` with `value` using a kernel
+// (not hipMemsetAsync, so the call is safe inside captured graphs).
+int fill(void* p, int64_t count, int elem_bytes, unsigned value, hipStream_t st);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -122,12 +122,8 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
   if (int rc = validate("pt_rmsnorm_bwd", rows, cols, x_dtype, w_dtype, true, &s)) return rc;
   hipStream_t st = as_stream(stream);
   if (rows == 0) {
-    if (dweight) {
-      // Empty batch: the weight gradient is a sum over no rows.
-      if (hipMemsetAsync(dweight, 0, static_cast<size_t>(cols) * dtype_size(w_dtype), st) !=
-          hipSuccess)
-        return fail(PT_EDEVICE, "pt_rmsnorm_bwd: hipMemsetAsync failed");
-    }
+    // Empty batch: the weight gradient is a sum over no rows.
+    if (dweight) return fill(dweight, cols, dtype_size(w_dtype), 0u, st);
     return ok();
   }
   if (!dy || !x || !weight || !rstd) return fail(PT_EINVAL, "pt_rmsnorm_bwd: null pointer");

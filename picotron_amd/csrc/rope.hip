@@ -226,7 +226,7 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
   if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > (1 << 20))
     return fail(PT_EINVAL, "pt_rope: head_dim must be a positive even number");
   if (!cos_table || !sin_table) return fail(PT_EINVAL, "pt_rope: null cos/sin table");
-  if (!x0 || !y0 || !desc0) return fail(PT_EINVAL, "pt_rope: null first tensor");
+  if (!desc0) return fail(PT_EINVAL, "pt_rope: null first tensor descriptor");
   if ((x1 == nullptr) != (y1 == nullptr) || (x1 != nullptr && desc1 == nullptr))
     return fail(PT_EINVAL, "pt_rope: second tensor needs x, y and desc");
   const int esize = dtype_size(dtype);
@@ -242,6 +242,8 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
     t1.n[0] = t1.n[1] = t1.n[2] = 1;
     t1.rows = 0;
   }
+  // Empty tensors may carry null data pointers; non-empty ones may not.
+  if (t0.rows > 0 && (!x0 || !y0)) return fail(PT_EINVAL, "pt_rope: null first tensor");
   const bool aligned = al0 && al1;
   if ((t0.rows + t1.rows) * (head_dim / 2) + 512 > 0xffffffffLL)
     return fail(PT_EUNSUPPORTED, "pt_rope: too many rows for one launch");

@@ -12,18 +12,26 @@ BF16 = dict(atol=2e-2, rtol=1.6e-2)
 FP16 = dict(atol=2e-3, rtol=2e-3)
 
 
-def close_fp32(actual: torch.Tensor, expected: torch.Tensor, rtol: float = 1e-5) -> None:
+def close_fp32(
+    actual: torch.Tensor, expected: torch.Tensor, rtol: float = 1e-5, scale: float | None = None
+) -> None:
+    """|a - e| <= rtol*|e| + 1e-6*scale.  ``scale`` defaults to max|e|; pass the magnitude of
+    the summands when the result is a near-cancelling difference of them."""
+
     expected = expected.to(actual.device)
-    scale = float(expected.abs().max()) if expected.numel() else 0.0
+    if scale is None:
+        scale = float(expected.abs().max()) if expected.numel() else 0.0
     torch.testing.assert_close(
         actual.double(), expected.double(), rtol=rtol, atol=max(1e-6 * scale, 1e-12)
     )
 
 
-def close(actual: torch.Tensor, expected: torch.Tensor, dtype: torch.dtype) -> None:
+def close(
+    actual: torch.Tensor, expected: torch.Tensor, dtype: torch.dtype, scale: float | None = None
+) -> None:
     expected = expected.to(actual.device)
     if dtype == torch.float32:
-        close_fp32(actual, expected)
+        close_fp32(actual, expected, scale=scale)
     elif dtype == torch.bfloat16:
         torch.testing.assert_close(actual.double(), expected.double(), **BF16)
     else:
