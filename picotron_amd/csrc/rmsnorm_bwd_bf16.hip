@@ -3,6 +3,6 @@
 
 namespace pt {
 namespace rmsnorm {
-template void launch_bwd<__bf16>(const BwdArgs&);
+template bool launch_bwd<__bf16>(const BwdArgs&);
 }  // namespace rmsnorm
 }  // namespace pt

@@ -3,6 +3,6 @@
 
 namespace pt {
 namespace rmsnorm {
-template void launch_bwd<float>(const BwdArgs&);
+template bool launch_bwd<float>(const BwdArgs&);
 }  // namespace rmsnorm
 }  // namespace pt

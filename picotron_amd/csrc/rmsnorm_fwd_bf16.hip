@@ -3,6 +3,6 @@
 
 namespace pt {
 namespace rmsnorm {
-template void launch_fwd<__bf16>(const FwdArgs&);
+template bool launch_fwd<__bf16>(const FwdArgs&);
 }  // namespace rmsnorm
 }  // namespace pt

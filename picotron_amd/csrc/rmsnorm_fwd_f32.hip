@@ -3,6 +3,6 @@
 
 namespace pt {
 namespace rmsnorm {
-template void launch_fwd<float>(const FwdArgs&);
+template bool launch_fwd<float>(const FwdArgs&);
 }  // namespace rmsnorm
 }  // namespace pt

@@ -21,6 +21,7 @@
 // atomics, so dW is bitwise reproducible for a given (rows, cols).
 #pragma once
 
+#include <cstdlib>
 #include <string>
 #include <type_traits>
 
@@ -29,11 +30,14 @@
 namespace pt {
 namespace rmsnorm {
 
-// Upper bound on weight-gradient partial rows (= blocks of the backward row pass).
-constexpr int64_t kMaxPartials = 512;
-// Waves per block for one-wave rows.
-constexpr int kFwdWavesWpr1 = 4;
-constexpr int kBwdWavesWpr1 = 8;
+// Waves per block: the backward uses 8 (one weight-gradient partial per 8 waves) and the
+// forward 4, or in both cases as many as a row spans when that is more.
+constexpr int kBwdWaves = 8;
+constexpr int kFwdWaves = 4;
+// Cache policy of the row streams (x, dy loads; y, dx stores): nontemporal accesses are
+// the measured optimum on MI355X for data read or written once per kernel.
+constexpr bool kLoadNT = true;
+constexpr bool kStoreNT = true;
 
 // ------------------------------------------------------------------ device helpers
 
@@ -86,8 +90,13 @@ struct RowRegs {
   }
 };
 
-// Loads the lane's VPL vectors of a row.  Out-of-range vectors are zero-filled.
-template <typename T, int VPL, int LANES, bool ALIGNED>
+// Loads the lane's VPL vectors of a row.  Aligned path: branch-free and unmasked -- a
+// lane whose vector lies past the row end loads the row's first vector instead, and the
+// caller ignores it (in_row()).  Nothing may consume the loaded registers here: loads
+// under divergent branches, or a select right after them, make the compiler wait for the
+// data at load time and so drain the next row's prefetch.  Element path: out-of-range
+// elements are zero-filled.
+template <typename T, int VPL, int LANES, bool ALIGNED, bool NT>
 __device__ __forceinline__ void load_row(const T* __restrict__ row, int rl, int cols,
                                          RowRegs<T, VPL>& r) {
   constexpr int V = Elem<T>::VEC;
@@ -96,11 +105,7 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int rl, int 
     const int e = (rl + k * LANES) * V;
     const int valid = cols - e;
     if constexpr (ALIGNED) {
-      if (valid > 0) {
-        r.v[k].raw = load16<false>(row + e);
-      } else {
-        r.v[k].raw = u32x4{0u, 0u, 0u, 0u};
-      }
+      r.v[k].raw = load16<NT>(row + (valid > 0 ? e : 0));
     } else {
 #pragma unroll
       for (int i = 0; i < V; ++i) {
@@ -110,155 +115,251 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int rl, int 
   }
 }
 
-template <typename T, int LANES, bool ALIGNED>
+template <typename T, int LANES, bool ALIGNED, bool NT>
 __device__ __forceinline__ void store_vec(T* __restrict__ row, int rl, int k, int cols,
                                           const float (&o)[Elem<T>::VEC]) {
   constexpr int V = Elem<T>::VEC;
   const int e = (rl + k * LANES) * V;
   const int valid = cols - e;
-  if (valid > 0) store_f32<T, ALIGNED>(row + e, o, valid);
+  if (valid > 0) store_f32<T, ALIGNED, NT>(row + e, o, valid);
 }
 
-// Sum over the WPR waves that share a row.  `red` holds 2*WPR floats, double buffered
-// by `parity` so consecutive rows need one barrier each.
-template <int WPR>
-__device__ __forceinline__ float row_sum(float v, float* red, int wave, int lane, int parity) {
+// True if vector k of lane rl lies inside the row (aligned path: whole vectors).
+template <typename T, int LANES>
+__device__ __forceinline__ bool in_row(int rl, int k, int cols) {
+  return (rl + k * LANES) * Elem<T>::VEC < cols;
+}
+
+// Sum over the WPR waves that share a row.  `red` holds 2*WAVES floats; `buf` alternates
+// between consecutive calls so one barrier per row suffices (a wave cannot overwrite a
+// buffer before every wave has passed the barrier of the call in between).  Waves sum the
+// partials of their row in wave order, so every wave of a row gets the same value.
+template <int WPR, int WAVES>
+__device__ __forceinline__ float row_sum(float v, float* red, int wave, int lane, int buf) {
   v = wave_sum(v);
   if constexpr (WPR > 1) {
-    float* buf = red + parity * WPR;
-    if (lane == 0) buf[wave] = v;
+    float* b = red + buf * WAVES;
+    if (lane == 0) b[wave] = v;
     __syncthreads();
+    const int first = (wave / WPR) * WPR;
     float t = 0.0f;
 #pragma unroll
-    for (int i = 0; i < WPR; ++i) t += buf[i];
+    for (int i = 0; i < WPR; ++i) t += b[first + i];
     v = t;
   }
   return v;
 }
 
 // ------------------------------------------------------------------ forward
+//
+// Row groups: a block has WAVES/WPR row slots; at step `it` block b works on the group of
+// rows starting at (it * gridDim.x + b) * slots, so at any moment all blocks work on one
+// compact window of rows (DRAM-friendly, like a non-persistent grid).  With a grid that
+// covers every row once (the default) each wave handles one row; smaller grids loop, and
+// the next row is then loaded into the second register buffer before the current one is
+// reduced.  Weights are loaded once per wave.
 
-template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED>
+template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
+          bool STORE_NT>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     const T* __restrict__ x, int64_t xs, const void* __restrict__ w, int wdt, T* __restrict__ y,
     int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps) {
-  static_assert(WPR == 1 || WPR == WAVES, "multi-wave rows use one row per block");
+  static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
   constexpr int LANES = 64 * WPR;
-  __shared__ float red[2 * WPR];
+  __shared__ float red[2 * WAVES];
 
   const int wave = threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
+  const int slot = wave / WPR;
   const int rl = (wave % WPR) * 64 + lane;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + wave / WPR;
-  // One-wave rows may have a partial last block; multi-wave rows launch exactly `rows`
-  // blocks, so every wave of a block reaches the barrier in row_sum.
-  if (WPR == 1 && row >= rows) return;
+  const int64_t group_stride = static_cast<int64_t>(gridDim.x) * RPB;
+  const int iters = static_cast<int>((rows + group_stride - 1) / group_stride);  // uniform
+  const int64_t r1 = rows;
+  const float inv_cols = 1.0f / static_cast<float>(cols);
 
-  RowRegs<T, VPL> xr;
-  load_row<T, VPL, LANES, ALIGNED>(x + row * xs, rl, cols, xr);
-
-  float ss = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float f = xr.at(k, i);
-      ss += f * f;
-    }
-  }
-  xr.opaque();
-  ss = row_sum<WPR>(ss, red, wave, lane, 0);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
-  if (rl == 0) rstd[row] = r;
-
-  T* yr = y + row * ys;
+  float wv[VPL][V];
 #pragma unroll
   for (int k = 0; k < VPL; ++k) {
     const int e = (rl + k * LANES) * V;
-    if (e >= cols) continue;
-    float wv[V];
-    load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv);
-    float o[V];
+    if (e < cols) {
+      load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv[k]);
+    } else {
 #pragma unroll
-    for (int i = 0; i < V; ++i) o[i] = (xr.at(k, i) * r) * wv[i];
-    store_vec<T, LANES, ALIGNED>(yr, rl, k, cols, o);
+      for (int i = 0; i < V; ++i) wv[k][i] = 0.0f;
+    }
+  }
+
+  auto process = [&](RowRegs<T, VPL>& xr, int64_t row, int buf) {
+    const bool active = row < r1;
+    float ss = 0.0f;
+    if (active) {
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float f = xr.at(k, i);
+          part += f * f;
+        }
+        ss += in_row<T, LANES>(rl, k, cols) ? part : 0.0f;
+      }
+    }
+    xr.opaque();
+    ss = row_sum<WPR, WAVES>(ss, red, wave, lane, buf);
+    if (!active) return;
+    const float r = 1.0f / sqrtf(ss * inv_cols + eps);
+    if (rl == 0) rstd[row] = r;
+    T* yr = y + row * ys;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      float o[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) o[i] = (xr.at(k, i) * r) * wv[k][i];
+      store_vec<T, LANES, ALIGNED, STORE_NT>(yr, rl, k, cols, o);
+    }
+  };
+
+  // Rows past the end are clamped to the last row for loading (keeping the loads
+  // unconditional) and skipped by process().
+  auto load = [&](RowRegs<T, VPL>& xr, int64_t row) {
+    load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + (row < r1 ? row : r1 - 1) * xs, rl, cols, xr);
+  };
+  RowRegs<T, VPL> a, b;
+  int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
+  load(a, ra);
+  for (int it = 0; it < iters; it += 2) {
+    const int64_t rb = ra + group_stride;
+    if (it + 1 < iters) load(b, rb);
+    process(a, ra, 0);
+    const int64_t rc = rb + group_stride;
+    if (it + 2 < iters) load(a, rc);
+    if (it + 1 < iters) process(b, rb, 1);
+    ra = rc;
   }
 }
 
 // ------------------------------------------------------------------ backward
+//
+// Persistent blocks walking the same interleaved row groups as the forward (step `it`:
+// rows (it * gridDim.x + b) * slots + slot), with the next row double-buffered in
+// registers.  Per row: dot = sum((g*w)*x) over the row (fp32, wave + LDS reduction),
+// dx = r*((g*w) - (x*r^2)*dm) written from the registers, and sum((g*x)*r) accumulated
+// per lane in fp32.  Spreading a row over WPR waves divides that accumulator (and the row
+// registers) by WPR.  At the end the row slots are combined in LDS in slot order and the
+// block writes one fp32 partial row; the partial count (the grid) is fixed for a given
+// shape and tuning, so the weight gradient is reproducible.
 
-template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED>
+template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
+          bool STORE_NT, bool PREFETCH = true>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, int64_t dys, const T* __restrict__ x, int64_t xs,
     const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* __restrict__ dx,
-    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols, int64_t rows_per_block) {
-  static_assert(WPR == 1 || WPR == WAVES, "multi-wave rows use one row per block");
+    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols) {
+  static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
   constexpr int LANES = 64 * WPR;
-  __shared__ float red[2 * WPR];
+  __shared__ float red[2 * WAVES];
   extern __shared__ float lds_dw[];  // [cols] when RPB > 1 and partial != nullptr
 
   const int wave = threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
   const int slot = wave / WPR;
   const int rl = (wave % WPR) * 64 + lane;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
-  const int64_t r1 = (r0 + rows_per_block < rows) ? r0 + rows_per_block : rows;
+  const int64_t group_stride = static_cast<int64_t>(gridDim.x) * RPB;
+  const int iters = static_cast<int>((rows + group_stride - 1) / group_stride);  // uniform
+  const int64_t r1 = rows;
   const bool want_dw = partial != nullptr;
   const float inv_cols = 1.0f / static_cast<float>(cols);
 
+  float wv[VPL][V];
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int e = (rl + k * LANES) * V;
+    if (e < cols) {
+      load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv[k]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; ++i) wv[k][i] = 0.0f;
+    }
+  }
   float acc[VPL][V];
 #pragma unroll
   for (int k = 0; k < VPL; ++k)
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
 
-  int parity = 0;
-  // Multi-wave rows: RPB == 1 and every wave of the block walks the same rows, so the
-  // barrier in row_sum is reached uniformly.
-  for (int64_t row = r0 + slot; row < r1; row += RPB) {
-    RowRegs<T, VPL> gr, xr;
-    load_row<T, VPL, LANES, ALIGNED>(dy + row * dys, rl, cols, gr);
-    load_row<T, VPL, LANES, ALIGNED>(x + row * xs, rl, cols, xr);
-    const float r = rstd[row];
-
+  struct Buf {
+    RowRegs<T, VPL> g, x;
+    float r;
+  };
+  // Rows past the end are clamped to the last row for loading (keeping the loads
+  // unconditional) and skipped by process().
+  auto load = [&](Buf& bf, int64_t row) {
+    const int64_t lr = row < r1 ? row : r1 - 1;
+    load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(dy + lr * dys, rl, cols, bf.g);
+    load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + lr * xs, rl, cols, bf.x);
+    bf.r = rstd[lr];
+  };
+  auto process = [&](Buf& bf, int64_t row, int buf) {
+    const bool active = row < r1;
     float dot = 0.0f;
+    if (active) {
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int e = (rl + k * LANES) * V;
-      if (e >= cols) continue;
-      float wv[V];
-      load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv);
+      for (int k = 0; k < VPL; ++k) {
+        float part = 0.0f;
 #pragma unroll
-      for (int i = 0; i < V; ++i) dot += (gr.at(k, i) * wv[i]) * xr.at(k, i);
+        for (int i = 0; i < V; ++i) part += (bf.g.at(k, i) * wv[k][i]) * bf.x.at(k, i);
+        dot += in_row<T, LANES>(rl, k, cols) ? part : 0.0f;
+      }
     }
-    gr.opaque();
-    xr.opaque();
-    dot = row_sum<WPR>(dot, red, wave, lane, parity);
-    parity ^= 1;
+    bf.g.opaque();
+    bf.x.opaque();
+    dot = row_sum<WPR, WAVES>(dot, red, wave, lane, buf);
+    if (!active) return;
+    const float r = bf.r;
     const float dm = dot * inv_cols;
     const float r2 = r * r;
-
-    T* dxr = dx + row * dxs;
+    if (dx != nullptr) {
+      T* dxr = dx + row * dxs;
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-      const int e = (rl + k * LANES) * V;
-      if (e >= cols) continue;
-      if (dx != nullptr) {
-        float wv[V];
-        load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv);
+      for (int k = 0; k < VPL; ++k) {
         float o[V];
 #pragma unroll
-        for (int i = 0; i < V; ++i) o[i] = r * (gr.at(k, i) * wv[i] - (xr.at(k, i) * r2) * dm);
-        store_vec<T, LANES, ALIGNED>(dxr, rl, k, cols, o);
+        for (int i = 0; i < V; ++i)
+          o[i] = r * (bf.g.at(k, i) * wv[k][i] - (bf.x.at(k, i) * r2) * dm);
+        store_vec<T, LANES, ALIGNED, STORE_NT>(dxr, rl, k, cols, o);
       }
-      if (want_dw) {
+    }
+    if (want_dw) {
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[k][i] += (gr.at(k, i) * xr.at(k, i)) * r;
-      }
+      for (int k = 0; k < VPL; ++k)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[k][i] += (bf.g.at(k, i) * bf.x.at(k, i)) * r;
+    }
+  };
+
+  int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
+  if constexpr (PREFETCH) {
+    Buf a, b;
+    load(a, ra);
+    for (int it = 0; it < iters; it += 2) {
+      const int64_t rb = ra + group_stride;
+      if (it + 1 < iters) load(b, rb);
+      process(a, ra, 0);
+      const int64_t rc = rb + group_stride;
+      if (it + 2 < iters) load(a, rc);
+      if (it + 1 < iters) process(b, rb, 1);
+      ra = rc;
+    }
+  } else {
+    for (int it = 0; it < iters; ++it) {
+      Buf a;
+      load(a, ra);
+      process(a, ra, it & 1);
+      ra += group_stride;
     }
   }
   if (!want_dw) return;
@@ -292,8 +393,10 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
   }
 }
 
-// dW[c] = sum_p partial[p][c] in increasing p, cast to the weight type.  A block covers
-// 64 columns; its 4 waves take p = wave, wave+4, ... and are combined in wave order.
+// dW[c] = sum_p partial[p][c] in a fixed order, cast to the weight type.  A block covers
+// kFinishCols columns with 8 groups of 32 lanes; group g sums p = g, g+8, ... (16 loads in
+// flight per lane), then the groups are added in group order.
+constexpr int kFinishCols = 32;
 __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
                                                                 int64_t nparts, int cols,
                                                                 void* __restrict__ dw, int wdt);
@@ -305,64 +408,115 @@ struct Shape {
   int wpr = 0;  // waves per row
 };
 
-// Chooses vectors-per-lane (a power of two, at least 4 once a row spans several waves)
-// and waves-per-row (1, 4 or 16) so one row fits in registers.  The backward holds dy,
-// x and the fp32 weight-gradient accumulator per lane, so it caps VPL at 8 below 16
-// waves per row.
-inline bool choose_shape(int64_t cols, int vec, bool backward, Shape* s) {
+// Launch tuning.  Defaults were chosen by measurement on MI355X; the environment can
+// override them (PT_RMSNORM_FWD_VPL_CAP, PT_RMSNORM_BWD_VPL_CAP, PT_RMSNORM_FWD_BLOCKS_PER_CU,
+// PT_RMSNORM_BWD_PARTIALS), read once per process.  The backward partial count fixes the
+// weight-gradient summation order, so dW is reproducible for a given setting.
+struct Tuning {
+  int fwd_vpl_cap = 4;
+  int bwd_vpl_cap = 2;
+  int64_t fwd_blocks_per_cu = 0;  // 0: no cap (one row per row slot)
+  int64_t bwd_partials = 512;
+};
+
+inline int64_t env_positive(const char* name, int64_t fallback) {
+  const char* v = std::getenv(name);
+  if (v == nullptr || *v == '\0') return fallback;
+  char* end = nullptr;
+  const long long x = std::strtoll(v, &end, 10);
+  return (end != v && x > 0) ? static_cast<int64_t>(x) : fallback;
+}
+
+inline const Tuning& tuning() {
+  static const Tuning t = [] {
+    Tuning d;
+    d.fwd_vpl_cap = static_cast<int>(env_positive("PT_RMSNORM_FWD_VPL_CAP", d.fwd_vpl_cap));
+    d.bwd_vpl_cap = static_cast<int>(env_positive("PT_RMSNORM_BWD_VPL_CAP", d.bwd_vpl_cap));
+    d.fwd_blocks_per_cu = env_positive("PT_RMSNORM_FWD_BLOCKS_PER_CU", d.fwd_blocks_per_cu);
+    d.bwd_partials = env_positive("PT_RMSNORM_BWD_PARTIALS", d.bwd_partials);
+    return d;
+  }();
+  return t;
+}
+
+inline int pow2_at_least(int64_t n) {
+  int v = 1;
+  while (v < n) v *= 2;
+  return v;
+}
+
+// Smallest waves-per-row in {1, 2, 4, 8, 16} whose vectors-per-lane fit under `cap`
+// (VPL a power of two); past that, 16 waves per row with up to 16 vectors per lane.
+inline bool choose_shape(int64_t cols, int vec, int cap, Shape* s) {
   const int64_t nvec = (cols + vec - 1) / vec;
-  const int wprs[3] = {1, 4, 16};
-  for (int wpr : wprs) {
+  for (int wpr = 1; wpr <= 16; wpr *= 2) {
     const int64_t per_lane = (nvec + 64 * wpr - 1) / (64 * wpr);
-    const int64_t cap = (backward && wpr < 16) ? 8 : 16;
-    if (per_lane > cap) continue;
-    int vpl = wpr == 1 ? 1 : 4;
-    while (vpl < per_lane) vpl *= 2;
-    *s = {vpl, wpr};
-    return true;
+    if (per_lane <= cap) {
+      *s = {pow2_at_least(per_lane), wpr};
+      return true;
+    }
   }
+  const int64_t per_lane = (nvec + 1023) / 1024;
+  if (per_lane > 16) return false;
+  *s = {pow2_at_least(per_lane), 16};
+  return true;
+}
+
+// The element-wise (unaligned) path is instantiated for fewer shapes: 4 waves per row
+// with 1..8 vectors per lane, or 16 waves per row with 8 or 16.
+inline Shape unaligned_shape(int64_t cols, int vec) {
+  const int64_t nvec = (cols + vec - 1) / vec;
+  const int64_t per4 = (nvec + 255) / 256;
+  if (per4 <= 8) return {pow2_at_least(per4), 4};
+  const int64_t per16 = (nvec + 1023) / 1024;
+  return {per16 <= 8 ? 8 : 16, 16};
+}
+
+// Calls f.template run<VPL, WPR>() for a runtime shape and returns true, or returns false
+// if that shape is not instantiated.  FULL selects the complete set (vector path);
+// otherwise the element-wise subset.
+template <bool FULL, typename F>
+bool dispatch_shape(const Shape& s, const F& f) {
+#define PT_RMS_CASE(V, W)            \
+  if (s.vpl == V && s.wpr == W) {    \
+    f.template run<V, W>();          \
+    return true;                     \
+  }
+  if constexpr (FULL) {
+    PT_RMS_CASE(1, 1) PT_RMS_CASE(2, 1) PT_RMS_CASE(4, 1) PT_RMS_CASE(8, 1)
+    PT_RMS_CASE(1, 2) PT_RMS_CASE(2, 2) PT_RMS_CASE(4, 2) PT_RMS_CASE(8, 2)
+    PT_RMS_CASE(1, 4) PT_RMS_CASE(2, 4) PT_RMS_CASE(4, 4) PT_RMS_CASE(8, 4)
+    PT_RMS_CASE(1, 8) PT_RMS_CASE(2, 8) PT_RMS_CASE(4, 8) PT_RMS_CASE(8, 8)
+    PT_RMS_CASE(1, 16) PT_RMS_CASE(2, 16) PT_RMS_CASE(4, 16) PT_RMS_CASE(8, 16)
+    PT_RMS_CASE(16, 16)
+  } else {
+    PT_RMS_CASE(1, 4) PT_RMS_CASE(2, 4) PT_RMS_CASE(4, 4) PT_RMS_CASE(8, 4)
+    PT_RMS_CASE(8, 16) PT_RMS_CASE(16, 16)
+  }
+#undef PT_RMS_CASE
   return false;
 }
 
-// Number of backward blocks (= weight-gradient partial rows) and rows per block.
-inline void bwd_grid(int64_t rows, const Shape& s, int64_t* blocks, int64_t* rpb) {
-  const int64_t slots = s.wpr == 1 ? kBwdWavesWpr1 : 1;
+inline int bwd_waves(const Shape& s) { return s.wpr > kBwdWaves ? s.wpr : kBwdWaves; }
+
+// Backward grid = number of weight-gradient partial rows.
+inline int64_t bwd_blocks(int64_t rows, const Shape& s) {
+  const int64_t slots = bwd_waves(s) / s.wpr;
   int64_t b = (rows + slots - 1) / slots;
-  if (b > kMaxPartials) b = kMaxPartials;
-  if (b < 1) b = 1;
-  const int64_t per = rows > 0 ? (rows + b - 1) / b : 1;
-  b = (rows + per - 1) / per;
-  if (b < 1) b = 1;
-  *blocks = b;
-  *rpb = per;
+  if (b > tuning().bwd_partials) b = tuning().bwd_partials;
+  return b < 1 ? 1 : b;
 }
 
-// Maps a runtime Shape onto the instantiated <VPL, WPR, WAVES> set and calls
-// f.template run<VPL, WPR, WAVES>().  WAVES_1 is the block size (in waves) for one-wave
-// rows; multi-wave rows use one row per block.
-template <int WAVES_1, typename F>
-void dispatch_shape(const Shape& s, const F& f) {
-  if (s.wpr == 1) {
-    switch (s.vpl) {
-      case 1: f.template run<1, 1, WAVES_1>(); break;
-      case 2: f.template run<2, 1, WAVES_1>(); break;
-      case 4: f.template run<4, 1, WAVES_1>(); break;
-      case 8: f.template run<8, 1, WAVES_1>(); break;
-      default: f.template run<16, 1, WAVES_1>(); break;
-    }
-  } else if (s.wpr == 4) {
-    switch (s.vpl) {
-      case 4: f.template run<4, 4, 4>(); break;
-      case 8: f.template run<8, 4, 4>(); break;
-      default: f.template run<16, 4, 4>(); break;
-    }
-  } else {
-    switch (s.vpl) {
-      case 4: f.template run<4, 16, 16>(); break;
-      case 8: f.template run<8, 16, 16>(); break;
-      default: f.template run<16, 16, 16>(); break;
-    }
-  }
+inline int fwd_waves(const Shape& s) { return s.wpr > kFwdWaves ? s.wpr : kFwdWaves; }
+
+// Forward grid: one row per row slot (non-persistent, measured fastest), optionally capped
+// at PT_RMSNORM_FWD_BLOCKS_PER_CU blocks per CU.
+inline int64_t fwd_blocks(int64_t rows, const Shape& s, int ncu) {
+  const int64_t slots = fwd_waves(s) / s.wpr;
+  int64_t b = (rows + slots - 1) / slots;
+  const int64_t per_cu = tuning().fwd_blocks_per_cu;
+  if (per_cu > 0 && b > static_cast<int64_t>(ncu) * per_cu) b = static_cast<int64_t>(ncu) * per_cu;
+  return b < 1 ? 1 : b;
 }
 
 struct FwdArgs {
@@ -379,6 +533,7 @@ struct FwdArgs {
   int xdt;
   bool aligned;
   Shape shape;
+  int64_t blocks;
   hipStream_t st;
 };
 
@@ -394,7 +549,6 @@ struct BwdArgs {
   int64_t dxs;
   float* partial;
   int64_t blocks;
-  int64_t rpb;
   int64_t rows;
   int cols;
   int xdt;
@@ -406,12 +560,11 @@ struct BwdArgs {
 template <typename T, typename WT, bool ALIGNED>
 struct FwdLaunch {
   const FwdArgs& a;
-  template <int VPL, int WPR, int WAVES>
+  template <int VPL, int WPR>
   void run() const {
-    constexpr int RPB = WAVES / WPR;
-    const int64_t blocks = (a.rows + RPB - 1) / RPB;
-    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED>),
-                       dim3(static_cast<unsigned>(blocks)), dim3(WAVES * 64), 0, a.st,
+    constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT>),
+                       dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
                        static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys,
                        a.rstd, a.rows, a.cols, a.eps);
   }
@@ -420,49 +573,48 @@ struct FwdLaunch {
 template <typename T, typename WT, bool ALIGNED>
 struct BwdLaunch {
   const BwdArgs& a;
-  template <int VPL, int WPR, int WAVES>
+  template <int VPL, int WPR>
   void run() const {
+    constexpr int WAVES = WPR > kBwdWaves ? WPR : kBwdWaves;
     constexpr int RPB = WAVES / WPR;
     const size_t lds =
         (RPB > 1 && a.partial != nullptr) ? static_cast<size_t>(a.cols) * sizeof(float) : 0;
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED>),
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT>),
                        dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
                        static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs,
                        a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
-                       a.cols, a.rpb);
+                       a.cols);
   }
 };
 
-// Per-storage-type launchers.  The vector path is instantiated for weights in
-// {x's type, fp32}; other weight types and unaligned rows take the element-wise path.
+// True when the 16-byte vector kernels apply: rows aligned (checked by the caller) and a
+// weight type with an instantiated vector path (x's type or fp32).
+inline bool vector_weight(int xdt, int wdt) { return wdt == xdt || wdt == PT_FLOAT32; }
+
+// Per-storage-type launchers; false if no kernel matched the shape (a bug, reported by
+// the caller as an error rather than silently skipping the launch).
 template <typename T>
-void launch_fwd(const FwdArgs& a) {
-  if (a.aligned && a.wdt == a.xdt) {
-    dispatch_shape<kFwdWavesWpr1>(a.shape, FwdLaunch<T, T, true>{a});
-  } else if (a.aligned && a.wdt == PT_FLOAT32) {
-    dispatch_shape<kFwdWavesWpr1>(a.shape, FwdLaunch<T, float, true>{a});
-  } else {
-    dispatch_shape<kFwdWavesWpr1>(a.shape, FwdLaunch<T, void, false>{a});
-  }
+bool launch_fwd(const FwdArgs& a) {
+  if (a.aligned && a.wdt == a.xdt) return dispatch_shape<true>(a.shape, FwdLaunch<T, T, true>{a});
+  if (a.aligned && a.wdt == PT_FLOAT32)
+    return dispatch_shape<true>(a.shape, FwdLaunch<T, float, true>{a});
+  return dispatch_shape<false>(a.shape, FwdLaunch<T, void, false>{a});
 }
 
 template <typename T>
-void launch_bwd(const BwdArgs& a) {
-  if (a.aligned && a.wdt == a.xdt) {
-    dispatch_shape<kBwdWavesWpr1>(a.shape, BwdLaunch<T, T, true>{a});
-  } else if (a.aligned && a.wdt == PT_FLOAT32) {
-    dispatch_shape<kBwdWavesWpr1>(a.shape, BwdLaunch<T, float, true>{a});
-  } else {
-    dispatch_shape<kBwdWavesWpr1>(a.shape, BwdLaunch<T, void, false>{a});
-  }
+bool launch_bwd(const BwdArgs& a) {
+  if (a.aligned && a.wdt == a.xdt) return dispatch_shape<true>(a.shape, BwdLaunch<T, T, true>{a});
+  if (a.aligned && a.wdt == PT_FLOAT32)
+    return dispatch_shape<true>(a.shape, BwdLaunch<T, float, true>{a});
+  return dispatch_shape<false>(a.shape, BwdLaunch<T, void, false>{a});
 }
 
-extern template void launch_fwd<float>(const FwdArgs&);
-extern template void launch_fwd<_Float16>(const FwdArgs&);
-extern template void launch_fwd<__bf16>(const FwdArgs&);
-extern template void launch_bwd<float>(const BwdArgs&);
-extern template void launch_bwd<_Float16>(const BwdArgs&);
-extern template void launch_bwd<__bf16>(const BwdArgs&);
+extern template bool launch_fwd<float>(const FwdArgs&);
+extern template bool launch_fwd<_Float16>(const FwdArgs&);
+extern template bool launch_fwd<__bf16>(const FwdArgs&);
+extern template bool launch_bwd<float>(const BwdArgs&);
+extern template bool launch_bwd<_Float16>(const BwdArgs&);
+extern template bool launch_bwd<__bf16>(const BwdArgs&);
 
 }  // namespace rmsnorm
 }  // namespace pt

@@ -47,7 +47,8 @@ def test_workspace_queries():
     lib = _lib.lib()
     # RMSNorm backward at 16384 x 4096: 512 partial rows of 4096 fp32
     assert lib.pt_rmsnorm_bwd_workspace_bytes(16384, 4096, _lib.PT_BFLOAT16) == 512 * 4096 * 4
-    assert lib.pt_rmsnorm_bwd_workspace_bytes(3, 128, _lib.PT_FLOAT32) == 1 * 128 * 4
+    # 3 rows: the element-wise path (2 rows per 8-wave block) needs 2 partial rows
+    assert lib.pt_rmsnorm_bwd_workspace_bytes(3, 128, _lib.PT_FLOAT32) == 2 * 128 * 4
     assert lib.pt_rmsnorm_bwd_workspace_bytes(0, 128, _lib.PT_FLOAT32) == 0
     assert lib.pt_cross_entropy_workspace_bytes(8192) == 16 + 8192 * 4
     assert lib.pt_adamw_block_elems() == 4096
