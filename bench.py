@@ -331,7 +331,7 @@ class CrossEntropyWorkload(Workload):
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         self.bytes_per_step = 2 * r * v * 2 + 16 * r
         self.tokens_per_step = r
-        self.dominant = "cross-entropy fused fwd+bwd (ce_prepare_kernel + ce_rows_kernel)"
+        self.dominant = "cross-entropy fused fwd+bwd (ce_prepare_kernel + ce_rows_kernel + ce_finish_kernel)"
         self.dominant_bytes = self.bytes_per_step
         self.description = (
             "fused cross-entropy fwd+bwd bf16 logits [8192, 128256] ~N(0,2^2), 410 targets = -100, "

@@ -6,16 +6,22 @@
 //   at cross_entropy.py:28-45 computes lse - logit[target] per row (forward only).
 //   Gradient of the mean: d/dx_j = (softmax_j - [j == target]) / n_valid, 0 on ignored rows.
 //
-// Passes per call:
-//   1. ce_prepare: one block counts non-ignored targets into the workspace (n_valid), and
-//      clears the completion ticket and the status word.  No host synchronisation.
-//   2. ce_rows: one workgroup per row.  The row is loaded once into registers (1024
-//      threads x VPT 16-byte vectors), reduced to max and sum(exp(x - max)) in fp32, and
-//      (if requested) the gradient is written over the logits from the same registers,
-//      so HBM sees exactly one read and one write of the logits.  Each row's fp32 loss
-//      goes to the workspace; the block that takes the last completion ticket sums them
-//      in a fixed order and writes the mean, so the loss is bitwise reproducible.
+// Three launches per call, no host synchronisation and no device-scope fences:
+//   1. ce_prepare: one block counts the non-ignored targets (n_valid) into the workspace
+//      and clears the status word.
+//   2. ce_rows: one 1024-thread workgroup per row.  The row is loaded once into registers
+//      (VPT 16-byte vectors per thread) and reduced to its max; exp(x - max) is then
+//      computed once per element, summed in fp32 and kept in the registers in place of the
+//      logit, so the gradient softmax / n_valid is written from registers without a second
+//      exponential: HBM sees one read and one write of the logits.  The target element's
+//      gradient (softmax_t - 1) / n_valid is computed from the exact fp32 target logit.
+//      Rows too long for registers, or not 16-byte aligned, use ce_rows_stream (online
+//      max / sum, then a second read).  Each row's fp32 loss goes to the workspace.
+//   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
+//      n_valid, so the loss is bitwise reproducible.
+// exp(x - m) is evaluated as exp2((x - m) * log2(e)) on the hardware exp2 unit.
 #include <cmath>
+#include <type_traits>
 
 #include "pt_common.hpp"
 
@@ -24,16 +30,27 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct CeWork {
-  float n_valid;     // number of non-ignored targets (exact below 2^24)
-  unsigned ticket;   // completion counter of ce_rows blocks
-  int status;        // bit 0: a non-ignored target outside [0, vocab)
+  float n_valid;  // number of non-ignored targets (exact below 2^24)
+  int reserved;
+  int status;     // bit 0: a non-ignored target outside [0, vocab)
   int pad;
   // followed by float row_loss[rows], 16-byte aligned
 };
 
 constexpr size_t kHeader = 16;
+
+__device__ __forceinline__ float* row_losses(CeWork* ws) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kHeader);
+}
+
+__device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// exp(x - m) on the hardware exp2 unit.  x - m is exact when x is within a factor of two of
+// m, so the row max contributes exactly 1 to the sum and a one-class row has loss 0.
+__device__ __forceinline__ float exp_shifted(float x, float m) { return exp2_((x - m) * kLog2e); }
 
 __device__ __forceinline__ float block_reduce_max(float v, float* red) {
   v = wave_max(v);
@@ -76,34 +93,27 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
   const float total = block_reduce_sum(cnt, red);
   if (threadIdx.x == 0) {
     ws->n_valid = total;
-    ws->ticket = 0u;
     ws->status = 0;
     if (rows == 0) *loss_out = NAN;  // mean over an empty batch: 0/0, as torch returns
   }
 }
 
-// exp(x) via the hardware exp2 unit: x * log2(e), then v_exp_f32.
-__device__ __forceinline__ float exp_(float x) { return __expf(x); }
-
-template <typename T, int VPT, bool ALIGNED>
-__global__ __launch_bounds__(kThreads) void ce_rows_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t os, int64_t is, int vocab,
-    const int64_t* __restrict__ targets, int64_t tos, int64_t tis, int64_t ignore_index,
-    int write_grad, CeWork* __restrict__ ws, float* __restrict__ loss_out, int64_t rows) {
-  constexpr int V = ALIGNED ? Elem<T>::VEC : 1;
-  __shared__ float red[kWaves];
-  __shared__ float s_target_logit;
-  __shared__ bool s_last;
-  float* row_loss = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kHeader);
-
+// Common start of both row kernels: locates the row and its target.  An ignored row gets a
+// zero gradient and a zero loss, and the function returns false.  Otherwise thread 0 reads
+// the target logit into *s_target_logit (NaN for a target outside [0, vocab), which also
+// sets status bit 0) before any thread of the block can overwrite the row: the block
+// passes at least two barriers before its first gradient store.
+template <typename T, int V, bool ALIGNED>
+__device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t os, int64_t is,
+                                             int vocab, const int64_t* targets, int64_t tos,
+                                             int64_t tis, int64_t ignore_index, int write_grad,
+                                             CeWork* ws, T** p_out, int* tgt_out,
+                                             float* s_target_logit) {
   const int64_t row = blockIdx.x;
   const int64_t o = row / inner, ii = row - (row / inner) * inner;
   T* p = logits + o * os + ii * is;
   const int64_t tgt = targets[o * tos + ii * tis];
-  const bool ignored = tgt == ignore_index;
-  const bool bad = !ignored && (tgt < 0 || tgt >= vocab);
-
-  if (ignored) {
+  if (tgt == ignore_index) {
     if (write_grad) {
       for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
         if constexpr (ALIGNED) {
@@ -113,191 +123,183 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
         }
       }
     }
-    if (threadIdx.x == 0) row_loss[row] = 0.0f;
-  } else {
-    if (threadIdx.x == 0) {
-      // Read before any thread of this block overwrites the row (barriers follow).
-      s_target_logit = bad ? NAN : Elem<T>::to_f32(p[tgt]);
-      if (bad) atomicOr(&ws->status, 1);
-    }
-    Vec16<T> v[VPT];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-      const int e = (threadIdx.x + k * kThreads) * V;
-      if constexpr (ALIGNED) {
-        if (e < vocab) {
-          v[k].raw = load16<true>(p + e);
-#pragma unroll
-          for (int i = 0; i < V; ++i) mx = fmaxf(mx, Elem<T>::to_f32(v[k].e[i]));
-        }
-      } else {
-        if (e < vocab) {
-          v[k].e[0] = p[e];
-          mx = fmaxf(mx, Elem<T>::to_f32(v[k].e[0]));
-        }
-      }
-    }
-    mx = block_reduce_max(mx, red);
-    float se = 0.0f;
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-      const int e = (threadIdx.x + k * kThreads) * V;
-      if (e < vocab) {
-#pragma unroll
-        for (int i = 0; i < V; ++i) se += exp_(Elem<T>::to_f32(v[k].e[i]) - mx);
-      }
-    }
-    se = block_reduce_sum(se, red);
-    const float lse = mx + __logf(se);
-    if (threadIdx.x == 0) row_loss[row] = lse - s_target_logit;
+    if (threadIdx.x == 0) row_losses(ws)[row] = 0.0f;
+    return false;
+  }
+  const bool bad = tgt < 0 || tgt >= vocab;
+  if (threadIdx.x == 0) {
+    *s_target_logit = bad ? NAN : Elem<T>::to_f32(p[tgt]);
+    if (bad) atomicOr(&ws->status, 1);
+  }
+  *p_out = p;
+  *tgt_out = bad ? -1 : static_cast<int>(tgt);
+  return true;
+}
 
-    if (write_grad) {
-      const float inv_n = 1.0f / ws->n_valid;
+// Row loss lse - x_t, written (max - x_t) + ln(sum exp(x - max)): exact when the target is
+// the row max and free of the cancellation of two large numbers.
+__device__ __forceinline__ float row_loss(float mx, float se, float xt) {
+  return (mx - xt) + __logf(se);
+}
+
+// Gradient of the target element, (softmax_t - 1) / n_valid, from the exact fp32 target
+// logit as exp(x_t - max) / sum: when softmax_t is close to 1 the difference x_t - max is
+// small and exact, so the result keeps fp32's relative accuracy (exactly 0 for one class).
+__device__ __forceinline__ float target_grad(float mx, float se, float xt, float inv_n) {
+  return (exp_shifted(xt, mx) / se - 1.0f) * inv_n;
+}
+
+// exp(x - max) is kept in the storage type in place of the logit.  fp16 holds it scaled by
+// 2^15 (at most 32768 < 65504), so that values down to 2^-29 keep full fp16 precision
+// instead of going subnormal; fp32 and bf16 have fp32's exponent range and need no scale.
+template <typename T>
+constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
+
+template <typename T, int VPT>
+__global__ __launch_bounds__(kThreads) void ce_rows_kernel(
+    T* __restrict__ logits, int64_t inner, int64_t os, int64_t is, int vocab,
+    const int64_t* __restrict__ targets, int64_t tos, int64_t tis, int64_t ignore_index,
+    int write_grad, CeWork* __restrict__ ws) {
+  constexpr int V = Elem<T>::VEC;
+  __shared__ float red[kWaves];
+  __shared__ float s_target_logit;
+  T* p = nullptr;
+  int tgt = 0;
+  if (!ce_row_begin<T, V, true>(logits, inner, os, is, vocab, targets, tos, tis, ignore_index,
+                                write_grad, ws, &p, &tgt, &s_target_logit))
+    return;
+
+  Vec16<T> v[VPT];
 #pragma unroll
-      for (int k = 0; k < VPT; ++k) {
-        const int e = (threadIdx.x + k * kThreads) * V;
-        if (e < vocab) {
-          float g[V];
+  for (int k = 0; k < VPT; ++k) {
+    const int e = (threadIdx.x + k * kThreads) * V;
+    if (e < vocab) v[k].raw = load16<true>(p + e);
+  }
+  float mx = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < V; ++i) {
-            const float pr = exp_(Elem<T>::to_f32(v[k].e[i]) - lse);
-            g[i] = (pr - ((e + i) == tgt ? 1.0f : 0.0f)) * inv_n;
-          }
-          if constexpr (ALIGNED) {
-            Vec16<T> out;
+  for (int k = 0; k < VPT; ++k) {
+    const int e = (threadIdx.x + k * kThreads) * V;
+    if (e < vocab) {
 #pragma unroll
-            for (int i = 0; i < V; ++i) out.e[i] = Elem<T>::from_f32(g[i]);
-            store16<true>(p + e, out.raw);
-          } else {
-            p[e] = Elem<T>::from_f32(g[0]);
-          }
-        }
+      for (int i = 0; i < V; ++i) mx = fmaxf(mx, Elem<T>::to_f32(v[k].e[i]));
+    }
+  }
+  mx = block_reduce_max(mx, red);
+  float se = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int e = (threadIdx.x + k * kThreads) * V;
+    if (e < vocab) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float ex = exp_shifted(Elem<T>::to_f32(v[k].e[i]), mx);
+        se += ex;
+        v[k].e[i] = Elem<T>::from_f32(ex * kExpScale<T>);
       }
     }
   }
+  se = block_reduce_sum(se, red);
+  const float xt = s_target_logit;
+  if (threadIdx.x == 0) row_losses(ws)[blockIdx.x] = row_loss(mx, se, xt);
+  if (!write_grad) return;
 
-  // Completion ticket: the last block to finish sums the per-row losses.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned t = atomicAdd(&ws->ticket, 1u);
-    s_last = (t == static_cast<unsigned>(rows - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  float acc = 0.0f;
-  for (int64_t r = threadIdx.x; r < rows; r += kThreads) acc += row_loss[r];
-  const float total = block_reduce_sum(acc, red);
-  if (threadIdx.x == 0) {
-    *loss_out = total / ws->n_valid;
-    ws->ticket = 0u;
+  const float inv_n = 1.0f / ws->n_valid;
+  const float scale = (inv_n / se) * (1.0f / kExpScale<T>);
+  const float gt = target_grad(mx, se, xt, inv_n);
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int e = (threadIdx.x + k * kThreads) * V;
+    if (e < vocab) {
+      float g[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) g[i] = Elem<T>::to_f32(v[k].e[i]) * scale;
+      if (static_cast<unsigned>(tgt - e) < static_cast<unsigned>(V)) {
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          if (e + i == tgt) g[i] = gt;
+      }
+      store_f32<T, true, true>(p + e, g, V);
+    }
   }
 }
 
-// Rows too long for registers (or not 16-byte aligned): pass 1 streams the row once
-// with an online max / sum-exp per thread; pass 2 re-reads it (mostly from L2 / MALL) to
-// write the gradient.
+// Rows too long for registers, or not 16-byte aligned: pass 1 streams the row once with an
+// online max / sum-exp per thread; pass 2 re-reads it (largely from L2 / MALL) to write the
+// gradient.
 template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
     T* __restrict__ logits, int64_t inner, int64_t os, int64_t is, int vocab,
     const int64_t* __restrict__ targets, int64_t tos, int64_t tis, int64_t ignore_index,
-    int write_grad, CeWork* __restrict__ ws, float* __restrict__ loss_out, int64_t rows) {
+    int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = ALIGNED ? Elem<T>::VEC : 1;
   __shared__ float red[kWaves];
   __shared__ float s_target_logit;
-  __shared__ bool s_last;
-  float* row_loss = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kHeader);
+  T* p = nullptr;
+  int tgt = 0;
+  if (!ce_row_begin<T, V, ALIGNED>(logits, inner, os, is, vocab, targets, tos, tis,
+                                   ignore_index, write_grad, ws, &p, &tgt, &s_target_logit))
+    return;
 
-  const int64_t row = blockIdx.x;
-  const int64_t o = row / inner, ii = row - (row / inner) * inner;
-  T* p = logits + o * os + ii * is;
-  const int64_t tgt = targets[o * tos + ii * tis];
-  const bool ignored = tgt == ignore_index;
-  const bool bad = !ignored && (tgt < 0 || tgt >= vocab);
+  auto load = [&](int e, float(&x)[V]) {
+    if constexpr (ALIGNED) {
+      Vec16<T> r;
+      r.raw = load16<false>(p + e);
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
+    } else {
+      x[0] = Elem<T>::to_f32(p[e]);
+    }
+  };
+  float m = -INFINITY, s = 0.0f;  // running max and sum of exp(x - m)
+  for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
+    float x[V];
+    load(e, x);
+    float mv = x[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i) mv = fmaxf(mv, x[i]);
+    if (mv > m) {
+      s *= exp_shifted(m, mv);
+      m = mv;
+    }
+    if (m == -INFINITY) continue;  // all -inf so far: nothing to add (and -inf - -inf is NaN)
+#pragma unroll
+    for (int i = 0; i < V; ++i) s += exp_shifted(x[i], m);
+  }
+  const float mx = block_reduce_max(m, red);
+  // rescale each thread's sum to the row max (threads without finite elements hold s = 0)
+  const float mine = (s > 0.0f) ? s * exp_shifted(m, mx) : 0.0f;
+  const float se = block_reduce_sum(mine, red);
+  const float xt = s_target_logit;
+  if (threadIdx.x == 0) row_losses(ws)[blockIdx.x] = row_loss(mx, se, xt);
+  if (!write_grad) return;
 
-  if (ignored) {
-    if (write_grad) {
-      for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
-        if constexpr (ALIGNED) {
-          store16<false>(p + e, u32x4{0u, 0u, 0u, 0u});
-        } else {
-          p[e] = Elem<T>::from_f32(0.0f);
-        }
-      }
-    }
-    if (threadIdx.x == 0) row_loss[row] = 0.0f;
-  } else {
-    if (threadIdx.x == 0) {
-      s_target_logit = bad ? NAN : Elem<T>::to_f32(p[tgt]);
-      if (bad) atomicOr(&ws->status, 1);
-    }
-    float m = -INFINITY, se = 0.0f;
-    for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
-      float x[V];
-      if constexpr (ALIGNED) {
-        load_f32<T, true>(p + e, x, V);
-      } else {
-        x[0] = Elem<T>::to_f32(p[e]);
-      }
-      float mv = x[0];
+  const float inv_n = 1.0f / ws->n_valid;
+  const float scale = inv_n / se;
+  const float gt = target_grad(mx, se, xt, inv_n);
+  for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
+    float x[V];
+    load(e, x);
+    float g[V];
 #pragma unroll
-      for (int i = 1; i < V; ++i) mv = fmaxf(mv, x[i]);
-      if (mv > m) {
-        se *= exp_(m - mv);
-        m = mv;
-      }
-#pragma unroll
-      for (int i = 0; i < V; ++i) se += exp_(x[i] - m);
-    }
-    const float mx = block_reduce_max(m, red);
-    // rescale each thread's partial sum to the row maximum (threads without elements
-    // hold m = -inf and se = 0, contributing 0)
-    const float mine = (se > 0.0f) ? se * exp_(m - mx) : 0.0f;
-    const float total = block_reduce_sum(mine, red);
-    const float lse = mx + __logf(total);
-    if (threadIdx.x == 0) row_loss[row] = lse - s_target_logit;
-
-    if (write_grad) {
-      const float inv_n = 1.0f / ws->n_valid;
-      for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
-        float x[V];
-        if constexpr (ALIGNED) {
-          load_f32<T, true>(p + e, x, V);
-        } else {
-          x[0] = Elem<T>::to_f32(p[e]);
-        }
-        float gr[V];
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          gr[i] = (exp_(x[i] - lse) - ((e + i) == tgt ? 1.0f : 0.0f)) * inv_n;
-        }
-        if constexpr (ALIGNED) {
-          store_f32<T, true>(p + e, gr, V);
-        } else {
-          p[e] = Elem<T>::from_f32(gr[0]);
-        }
-      }
+    for (int i = 0; i < V; ++i) g[i] = (e + i == tgt) ? gt : exp_shifted(x[i], mx) * scale;
+    if constexpr (ALIGNED) {
+      store_f32<T, true>(p + e, g, V);
+    } else {
+      p[e] = Elem<T>::from_f32(g[0]);
     }
   }
+}
 
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned t = atomicAdd(&ws->ticket, 1u);
-    s_last = (t == static_cast<unsigned>(rows - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+// loss = sum(row_loss) / n_valid, summed by one block in a fixed order.
+__global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict__ ws,
+                                                              int64_t rows,
+                                                              float* __restrict__ loss_out) {
+  __shared__ float red[kWaves];
+  const float* rl = row_losses(ws);
   float acc = 0.0f;
-  for (int64_t r = threadIdx.x; r < rows; r += kThreads) acc += row_loss[r];
+  for (int64_t r = threadIdx.x; r < rows; r += kThreads) acc += rl[r];
   const float total = block_reduce_sum(acc, red);
-  if (threadIdx.x == 0) {
-    *loss_out = total / ws->n_valid;
-    ws->ticket = 0u;
-  }
+  if (threadIdx.x == 0) *loss_out = total / ws->n_valid;
 }
 
 // In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1.
@@ -328,46 +330,44 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
   }
 }
 
-template <typename T, int VPT, bool ALIGNED>
+template <typename T, int VPT>
 void launch_rows(void* logits, int64_t inner, int64_t os, int64_t is, int vocab,
                  const int64_t* targets, int64_t tos, int64_t tis, int64_t ignore_index,
-                 int write_grad, CeWork* ws, float* loss_out, int64_t rows, hipStream_t st) {
-  hipLaunchKernelGGL((ce_rows_kernel<T, VPT, ALIGNED>), dim3(static_cast<unsigned>(rows)),
-                     dim3(kThreads), 0, st, static_cast<T*>(logits), inner, os, is, vocab,
-                     targets, tos, tis, ignore_index, write_grad, ws, loss_out, rows);
+                 int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
+  hipLaunchKernelGGL((ce_rows_kernel<T, VPT>), dim3(static_cast<unsigned>(rows)), dim3(kThreads),
+                     0, st, static_cast<T*>(logits), inner, os, is, vocab, targets, tos, tis,
+                     ignore_index, write_grad, ws);
 }
 
+// Register-resident rows for up to 16 vectors per thread (131072 fp16/bf16 or 65536 fp32
+// elements); longer or unaligned rows stream.
 template <typename T>
-int dispatch_rows(bool aligned, void* logits, int64_t inner, int64_t os, int64_t is, int vocab,
-                  const int64_t* targets, int64_t tos, int64_t tis, int64_t ignore_index,
-                  int write_grad, CeWork* ws, float* loss_out, int64_t rows, hipStream_t st) {
-  const int V = aligned ? Elem<T>::VEC : 1;
-  const int64_t per_thread = (static_cast<int64_t>(vocab) + int64_t{kThreads} * V - 1) /
-                             (int64_t{kThreads} * V);
-#define PT_CE_CASE(N)                                                                         \
-  if (per_thread <= N) {                                                                      \
-    launch_rows<T, N, true>(logits, inner, os, is, vocab, targets, tos, tis, ignore_index,    \
-                            write_grad, ws, loss_out, rows, st);                              \
-    return PT_OK;                                                                             \
-  }
+void dispatch_rows(bool aligned, void* logits, int64_t inner, int64_t os, int64_t is, int vocab,
+                   const int64_t* targets, int64_t tos, int64_t tis, int64_t ignore_index,
+                   int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
+  const int64_t per_thread = (static_cast<int64_t>(vocab) + int64_t{kThreads} * Elem<T>::VEC - 1) /
+                             (int64_t{kThreads} * Elem<T>::VEC);
   if (aligned) {
+#define PT_CE_CASE(N)                                                                        \
+  if (per_thread <= N) {                                                                     \
+    launch_rows<T, N>(logits, inner, os, is, vocab, targets, tos, tis, ignore_index,         \
+                      write_grad, ws, rows, st);                                             \
+    return;                                                                                  \
+  }
     PT_CE_CASE(1)
     PT_CE_CASE(2)
     PT_CE_CASE(4)
     PT_CE_CASE(8)
     PT_CE_CASE(16)
-  }
 #undef PT_CE_CASE
-  if (aligned) {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<T*>(logits), inner, os, is, vocab,
-                       targets, tos, tis, ignore_index, write_grad, ws, loss_out, rows);
+                       targets, tos, tis, ignore_index, write_grad, ws);
   } else {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, false>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<T*>(logits), inner, os, is, vocab,
-                       targets, tos, tis, ignore_index, write_grad, ws, loss_out, rows);
+                       targets, tos, tis, ignore_index, write_grad, ws);
   }
-  return PT_OK;
 }
 
 }  // namespace
@@ -414,25 +414,21 @@ int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_s
   const bool aligned = aligned16(logits) && (vocab * esize) % 16 == 0 &&
                        (outer <= 1 || (outer_stride * esize) % 16 == 0) &&
                        (inner <= 1 || (inner_stride * esize) % 16 == 0);
-  int rc;
   const int v = static_cast<int>(vocab);
   if (dtype == PT_FLOAT32) {
-    rc = dispatch_rows<float>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
-                              t_outer_stride, t_inner_stride, ignore_index, write_grad, ws,
-                              loss_out, rows, st);
+    dispatch_rows<float>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
+                         t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows, st);
   } else if (dtype == PT_FLOAT16) {
-    rc = dispatch_rows<_Float16>(aligned, logits, inner_nz, outer_stride, inner_stride, v,
-                                 targets, t_outer_stride, t_inner_stride, ignore_index,
-                                 write_grad, ws, loss_out, rows, st);
+    dispatch_rows<_Float16>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
+                            t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows,
+                            st);
   } else {
-    rc = dispatch_rows<__bf16>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
-                               t_outer_stride, t_inner_stride, ignore_index, write_grad, ws,
-                               loss_out, rows, st);
+    dispatch_rows<__bf16>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
+                          t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows, st);
   }
-  if (rc != PT_OK)
-    return fail(rc, "pt_cross_entropy: vocab " + std::to_string(vocab) +
-                        " exceeds the register-resident row capacity");
-  return check_launch("pt_cross_entropy");
+  if (int rc = check_launch("pt_cross_entropy (rows)")) return rc;
+  hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(kThreads), 0, st, ws, rows, loss_out);
+  return check_launch("pt_cross_entropy (finish)");
 }
 
 int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,

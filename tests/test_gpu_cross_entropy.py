@@ -92,6 +92,26 @@ def test_shapes(gpu, dtype, rows, vocab):
     _check(logits, targets, dtype)
 
 
+@pytest.mark.parametrize(
+    "dtype,vocab",
+    [(torch.bfloat16, 4096), (torch.bfloat16, 262144), (torch.float32, 1001), (torch.float16, 50257)],
+)
+def test_masked_logits(gpu, dtype, vocab):
+    # -inf logits (masked vocabulary padding) contribute 0 to the softmax and get a zero
+    # gradient; the masked tail covers whole per-thread chunks of every kernel variant.
+    rows = 6
+    logits = randn((rows, vocab), dtype, gpu, vocab + 7, 2.0)
+    keep = vocab * 3 // 5
+    logits[:, keep:] = float("-inf")
+    logits[:, 1::7] = float("-inf")
+    g = torch.Generator(device=gpu).manual_seed(vocab + 8)
+    targets = torch.randint(0, keep, (rows,), generator=g, device=gpu)
+    targets = torch.where(targets % 7 == 1, targets - 1, targets)  # never a masked target
+    buf = _check(logits, targets, dtype)
+    assert bool((buf[:, keep:] == 0).all())
+    assert bool(torch.isfinite(buf).all())
+
+
 def test_train_loop_view(gpu):
     # loss(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:]) on (B, S, V) bf16 logits
     b, s, v = 2, 65, 3000
