@@ -10,9 +10,9 @@ namespace rmsnorm {
 __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
                                                                 int64_t nparts, int cols,
                                                                 void* __restrict__ dw, int wdt) {
-  constexpr int kGroups = 256 / kFinishCols;  // 8
+  constexpr int kGroups = 256 / kFinishCols;
   constexpr int kUnroll = 16;
-  __shared__ float lds[kGroups][kFinishCols];
+  __shared__ float lds[kGroups][kFinishCols + 1];
   const int col = threadIdx.x % kFinishCols;
   const int grp = threadIdx.x / kFinishCols;
   const int c = blockIdx.x * kFinishCols + col;
@@ -54,7 +54,8 @@ int validate(const char* fn, int64_t rows, int64_t cols, int xdt, int wdt, bool 
     return fail(PT_EINVAL, std::string(fn) + ": unknown dtype code");
   if (rows < 0 || cols <= 0)
     return fail(PT_EINVAL, std::string(fn) + ": rows must be >= 0 and cols > 0");
-  if (rows > (int64_t{1} << 40)) return fail(PT_EUNSUPPORTED, std::string(fn) + ": rows too large");
+  // Bounds the per-block row-group count (an int) for any grid.
+  if (rows > (int64_t{1} << 36)) return fail(PT_EUNSUPPORTED, std::string(fn) + ": rows too large");
   const int vec = 16 / dtype_size(xdt);
   const int cap = cap_of(backward ? tuning().bwd_vpl_cap : tuning().fwd_vpl_cap);
   if (!choose_shape(cols, vec, cap, s))

@@ -38,6 +38,8 @@ constexpr int kFwdWaves = 4;
 // the measured optimum on MI355X for data read or written once per kernel.
 constexpr bool kLoadNT = true;
 constexpr bool kStoreNT = true;
+// Rows the backward keeps in flight ahead of the one it is reducing (0, 1 or 2).
+constexpr int kBwdPrefetch = 1;
 
 // ------------------------------------------------------------------ device helpers
 
@@ -70,6 +72,24 @@ __device__ __forceinline__ void load_weight(const void* w, int wdt, int64_t e, i
     const WT* p = reinterpret_cast<const WT*>(w) + e;
 #pragma unroll
     for (int i = 0; i < N; ++i) out[i] = (i < valid) ? static_cast<float>(p[i]) : 0.0f;
+  }
+}
+
+// Loads the weights of a lane's VPL vectors as fp32.  Vector path: branch-free -- a vector
+// past the row end loads the row's first weights instead (its products are never stored
+// or summed), so the loads issue back to back and their one wait comes at first use.
+// Element path: zero past the row end.
+template <typename WT, int VPL, int N, bool VECTOR>
+__device__ __forceinline__ void load_lane_weights(const void* w, int wdt, int rl, int lanes,
+                                                  int cols, float (&wv)[VPL][N]) {
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int e = (rl + k * lanes) * N;
+    if constexpr (VECTOR) {
+      load_weight<WT, N, true>(w, wdt, e < cols ? e : 0, N, wv[k]);
+    } else {
+      load_weight<WT, N, false>(w, wdt, e, cols - e, wv[k]);
+    }
   }
 }
 
@@ -163,7 +183,7 @@ template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bo
           bool STORE_NT>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     const T* __restrict__ x, int64_t xs, const void* __restrict__ w, int wdt, T* __restrict__ y,
-    int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps) {
+    int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps, int iters) {
   static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
@@ -174,22 +194,13 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
   const int lane = threadIdx.x % 64;
   const int slot = wave / WPR;
   const int rl = (wave % WPR) * 64 + lane;
+  // iters = ceil(rows / group_stride), computed on the host: the same for every wave.
   const int64_t group_stride = static_cast<int64_t>(gridDim.x) * RPB;
-  const int iters = static_cast<int>((rows + group_stride - 1) / group_stride);  // uniform
   const int64_t r1 = rows;
   const float inv_cols = 1.0f / static_cast<float>(cols);
 
   float wv[VPL][V];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int e = (rl + k * LANES) * V;
-    if (e < cols) {
-      load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv[k]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) wv[k][i] = 0.0f;
-    }
-  }
+  load_lane_weights<WT, VPL, V, ALIGNED>(w, wdt, rl, LANES, cols, wv);
 
   auto process = [&](RowRegs<T, VPL>& xr, int64_t row, int buf) {
     const bool active = row < r1;
@@ -252,11 +263,11 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
 // shape and tuning, so the weight gradient is reproducible.
 
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT, bool PREFETCH = true>
+          bool STORE_NT, int PREFETCH = kBwdPrefetch>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, int64_t dys, const T* __restrict__ x, int64_t xs,
     const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* __restrict__ dx,
-    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols) {
+    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols, int iters) {
   static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
@@ -268,23 +279,14 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
   const int lane = threadIdx.x % 64;
   const int slot = wave / WPR;
   const int rl = (wave % WPR) * 64 + lane;
+  // iters = ceil(rows / group_stride), computed on the host: the same for every wave.
   const int64_t group_stride = static_cast<int64_t>(gridDim.x) * RPB;
-  const int iters = static_cast<int>((rows + group_stride - 1) / group_stride);  // uniform
   const int64_t r1 = rows;
   const bool want_dw = partial != nullptr;
   const float inv_cols = 1.0f / static_cast<float>(cols);
 
   float wv[VPL][V];
-#pragma unroll
-  for (int k = 0; k < VPL; ++k) {
-    const int e = (rl + k * LANES) * V;
-    if (e < cols) {
-      load_weight<WT, V, ALIGNED>(w, wdt, e, cols - e, wv[k]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i) wv[k][i] = 0.0f;
-    }
-  }
+  load_lane_weights<WT, VPL, V, ALIGNED>(w, wdt, rl, LANES, cols, wv);
   float acc[VPL][V];
 #pragma unroll
   for (int k = 0; k < VPL; ++k)
@@ -342,7 +344,31 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
   };
 
   int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
-  if constexpr (PREFETCH) {
+  if constexpr (PREFETCH == 2) {
+    // Two rows in flight ahead of the one being reduced.  Consecutive reductions alternate
+    // the two LDS scratch buffers of row_sum.
+    Buf a, b, c;
+    load(a, ra);
+    if (1 < iters) load(b, ra + group_stride);
+    int rb = 0;
+    for (int it = 0; it < iters; it += 3) {
+      const int64_t r1n = ra + group_stride, r2n = ra + 2 * group_stride;
+      if (it + 2 < iters) load(c, r2n);
+      process(a, ra, rb);
+      rb ^= 1;
+      if (it + 3 < iters) load(a, ra + 3 * group_stride);
+      if (it + 1 < iters) {
+        process(b, r1n, rb);
+        rb ^= 1;
+      }
+      if (it + 4 < iters) load(b, ra + 4 * group_stride);
+      if (it + 2 < iters) {
+        process(c, r2n, rb);
+        rb ^= 1;
+      }
+      ra += 3 * group_stride;
+    }
+  } else if constexpr (PREFETCH == 1) {
     Buf a, b;
     load(a, ra);
     for (int it = 0; it < iters; it += 2) {
@@ -394,8 +420,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
 }
 
 // dW[c] = sum_p partial[p][c] in a fixed order, cast to the weight type.  A block covers
-// kFinishCols columns with 8 groups of 32 lanes; group g sums p = g, g+8, ... (16 loads in
-// flight per lane), then the groups are added in group order.
+// kFinishCols columns with 8 groups of 32 lanes; group g sums p = g, g+8, ... in increasing
+// p (16 loads in flight per lane), then the groups are added in group order.
 constexpr int kFinishCols = 32;
 __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
                                                                 int64_t nparts, int cols,
@@ -519,6 +545,12 @@ inline int64_t fwd_blocks(int64_t rows, const Shape& s, int ncu) {
   return b < 1 ? 1 : b;
 }
 
+// Row-group steps of a grid of `blocks` blocks with `slots` row slots each.
+inline int row_iters(int64_t rows, int64_t blocks, int slots) {
+  const int64_t stride = blocks * slots;
+  return static_cast<int>((rows + stride - 1) / stride);
+}
+
 struct FwdArgs {
   const void* x;
   int64_t xs;
@@ -566,7 +598,7 @@ struct FwdLaunch {
     hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT>),
                        dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
                        static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys,
-                       a.rstd, a.rows, a.cols, a.eps);
+                       a.rstd, a.rows, a.cols, a.eps, row_iters(a.rows, a.blocks, WAVES / WPR));
   }
 };
 
@@ -583,7 +615,7 @@ struct BwdLaunch {
                        dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
                        static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs,
                        a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
-                       a.cols);
+                       a.cols, row_iters(a.rows, a.blocks, RPB));
   }
 };
 
