@@ -11,10 +11,12 @@ Infinity Cache).  Inputs are synthetic (seeded N(0,1), weight 1 + 0.02 N(0,1)) a
 resident in HBM before timing.
 
 Prints ONE JSON line: value = algorithmic bytes of the step / wall time of the step
-(decimal GB/s), with a ``roofline`` object for the dominant kernel (HIP events around each
-of its launches inside the timed region) and a ``cpu_baseline`` object (the reference's
-PyTorch fallback, restated in ``oracle/``, timed on this host's cores on a bounded sample
-of the same inputs).
+(decimal GB/s) over K timed steps bracketed by device synchronisations, with a
+``roofline`` object for the dominant kernel (HIP events around each of its launches, on
+the stream they run on, over a second pass of the same K steps -- the event records cost a
+few microseconds per launch, so that pass is kept out of the value) and a ``cpu_baseline``
+object (the reference's PyTorch fallback, restated in ``oracle/``, timed on this host's
+cores on a bounded sample of the same inputs).
 """
 
 from __future__ import annotations
@@ -68,16 +70,21 @@ def _cpu_info() -> tuple[int, int, str]:
     return cores, os.cpu_count() or cores, model
 
 
-def _time_cpu(fn, target_s: float = 2.0) -> float:
-    """Median of 3 timed calls after one warm-up (seconds per call)."""
+CPU_TARGET_S = 10.0  # CPU work per baseline measurement
+
+
+def _time_cpu(fn, target_s: float = CPU_TARGET_S) -> tuple[float, int]:
+    """(median seconds per call, calls timed): one warm-up call, then calls until about
+    ``target_s`` seconds of CPU work (at least 3)."""
 
     fn()
     times = []
-    for _ in range(3):
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < target_s and len(times) < 1000):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
-    return statistics.median(times)
+    return statistics.median(times), len(times)
 
 
 # ------------------------------------------------------------------ workloads
@@ -162,15 +169,16 @@ class RMSNormWorkload(Workload):
 
         cores, _, _ = _cpu_info()
         torch.set_num_threads(cores)
-        rows = 2048
-        x, dy, w = self.x[0][:rows].cpu(), self.dy[0][:rows].cpu(), self.w.cpu()
-        sec = _time_cpu(lambda: o_rms.fallback_forward_backward(x, w, self.eps, dy))
+        rows = self.rows
+        x, dy, w = self.x[0].cpu(), self.dy[0].cpu(), self.w.cpu()
+        sec, calls = _time_cpu(lambda: o_rms.fallback_forward_backward(x, w, self.eps, dy))
         c = self.cols
         nbytes = 5 * rows * c * 2 + 3 * c * 2 + 8 * rows
         return dict(
             value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
-            sample=f"first {rows} of 16384 rows (1/8 of one activation): reference PyTorch fallback "
-                   f"fwd+bwd (rmsnorm.py:56-60,113-134) on bf16 CPU tensors, median of 3 after 1 warm-up",
+            sample=f"one activation [{rows}, {c}] (one of the step's {self.layers} layers): reference PyTorch "
+                   f"fallback fwd+bwd (rmsnorm.py:56-60,113-134) on bf16 CPU tensors, median of {calls} calls "
+                   f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
 
@@ -224,14 +232,15 @@ class SwiGLUWorkload(Workload):
 
         cores, _, _ = _cpu_info()
         torch.set_num_threads(cores)
-        rows = 512
+        rows = self.rows
         n = rows * self.cols
         g, u, dy = self.g[0][:n].cpu(), self.u[0][:n].cpu(), self.dy[0][:n].cpu()
-        sec = _time_cpu(lambda: o_swiglu.fallback_forward_backward(g, u, dy))
+        sec, calls = _time_cpu(lambda: o_swiglu.fallback_forward_backward(g, u, dy))
         return dict(
             value=8 * n * 2 / sec / 1e9, unit="GB/s", cores=cores, kind="port",
-            sample=f"first {rows} of 16384 token rows: reference PyTorch fallback fwd+bwd (F.silu*up, "
-                   f"swiglu.py:75-81) on bf16 CPU tensors, median of 3 after 1 warm-up",
+            sample=f"one layer [{rows}, {self.cols}]: reference PyTorch fallback fwd+bwd "
+                   f"(F.silu*up, swiglu.py:75-81) on bf16 CPU tensors, median of {calls} calls "
+                   f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
 
@@ -298,17 +307,18 @@ class RoPEWorkload(Workload):
 
         cores, _, _ = _cpu_info()
         torch.set_num_threads(cores)
-        bsz = 1
+        bsz = 8
         q = self.q[0][:bsz].cpu()
         dq = self.dq[0][:bsz].cpu()
         cos, sin = self.cos.cpu().bfloat16(), self.sin.cpu().bfloat16()
-        sec = _time_cpu(lambda: o_rope.fallback_forward_backward(q, cos, sin, dq))
+        sec, calls = _time_cpu(lambda: o_rope.fallback_forward_backward(q, cos, sin, dq))
         nbytes = 4 * q.numel() * 2
         return dict(
             value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
-            sample="query of batch element 0 (1/8 of q): reference eager apply_rotary_embedding "
-                   "(rope.py:35-51, interleaved, bf16 tables) fwd + autograd bwd on CPU, median of 3",
-            seconds_per_call=sec, tokens_per_s=2048 / sec,
+            sample=f"the query [{bsz}, 32, 2048, 128] of one layer (k excluded): reference eager apply_rotary_embedding "
+                   f"(rope.py:35-51, interleaved, bf16 tables) fwd + autograd bwd on CPU, median of {calls} "
+                   f"calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=bsz * 2048 / sec,
         )
 
 
@@ -357,14 +367,15 @@ class CrossEntropyWorkload(Workload):
 
         cores, _, _ = _cpu_info()
         torch.set_num_threads(cores)
-        rows = 256
+        rows = 1024
         logits = _seeded((rows, self.vocab), torch.bfloat16, 100, 2.0).cpu()
         targets = self.targets[:rows].cpu()
-        sec = _time_cpu(lambda: o_ce.fallback_forward_backward(logits, targets))
+        sec, calls = _time_cpu(lambda: o_ce.fallback_forward_backward(logits, targets))
         return dict(
             value=(2 * rows * self.vocab * 2 + 16 * rows) / sec / 1e9, unit="GB/s", cores=cores, kind="port",
             sample=f"{rows} of 8192 rows: F.cross_entropy fwd + autograd bwd on the fp32 upcast (the "
-                   f"reference fallback under autocast), median of 3",
+                   f"reference fallback under autocast), median of {calls} calls (~{CPU_TARGET_S:.0f} s) "
+                   f"after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
 
@@ -412,15 +423,16 @@ class AdamWWorkload(Workload):
     def cpu_baseline(self) -> dict:
         cores, _, _ = _cpu_info()
         torch.set_num_threads(cores)
-        n = 50_000_000
+        n = 120_000_000
         p = torch.nn.Parameter(self.p[:n].cpu())
         p.grad = self.g[:n].cpu()
         opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
-        sec = _time_cpu(opt.step)
+        sec, calls = _time_cpu(opt.step)
         return dict(
             value=28 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
-            sample=f"{n:.0e} of 1.2e9 params: torch.optim.AdamW(foreach=False).step() (the reference "
-                   f"fallback, adamw.py:47) on CPU, median of 3 after 1 warm-up",
+            sample=f"{n:.1e} of 1.2e9 params (1/10): torch.optim.AdamW(foreach=False).step() (the reference "
+                   f"fallback, adamw.py:47) on CPU, median of {calls} calls (~{CPU_TARGET_S:.0f} s) after "
+                   f"1 warm-up",
             seconds_per_call=sec, params_per_s=n / sec,
         )
 
@@ -511,16 +523,28 @@ def main() -> int:
         wl.step(None)
     torch.cuda.synchronize()
 
+    # Pass 1 (the reported value): K steps, nothing but the workload's own launches between
+    # the two synchronisations.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.step(None)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    # Pass 2 (the roofline): the same K steps again with a HIP event pair around every
+    # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
+    # records add a few microseconds per launch, so this pass is not used for the value.
     per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "adamw": 1, "copy": layers}[args.workload]
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps * per_step)]
     pending = list(reversed(events))
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    t1 = time.perf_counter()
     for _ in range(args.steps):
         wl.step(pending)
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    elapsed_instrumented = time.perf_counter() - t1
 
     ms_per_step = elapsed / args.steps * 1e3
     gbps = wl.bytes_per_step / (elapsed / args.steps) / 1e9
@@ -540,6 +564,8 @@ def main() -> int:
         "avg_launch_us": round(avg_us, 2),
         "median_launch_us": round(statistics.median(launch_ms) * 1e3, 2),
         "launches_timed": len(launch_ms),
+        "timing": "HIP events around each launch, in a second pass of the same steps",
+        "ms_per_step_with_events": round(elapsed_instrumented / args.steps * 1e3, 4),
     }
     if traffic:
         roofline["traffic_source"] = traffic.get("source")

@@ -51,7 +51,7 @@ const char* pt_last_error(void);
 /* 1 if `device` is a gfx950 GPU this library was built for, 0 otherwise.
  * Replaces the capability gate of src/picotron/utils/hardware.py:93-108
  * (detect_triton_support: capability >= 7) and the per-op checks at
- * src/picotron/nn/triton_kernels/rmsnorm.py:185-186, swiglu.py:303-304. */
+ * src/picotron/nn/triton_kernels/rmsnorm.py:142-145, swiglu.py:89-92. */
 int pt_device_supported(int device);
 
 /* ---------------------------------------------------------------- RMSNorm

@@ -1,7 +1,7 @@
 """Shared launch gate for the fused kernels: library loaded, GPU tensors, gfx950 device.
 
 Replaces the Triton checks of the reference (``_TRITON_AVAILABLE``, ``is_cuda``,
-``get_device_capability(...)[0] >= 7``; e.g. src/picotron/nn/triton_kernels/rmsnorm.py:181-186).
+``get_device_capability(...)[0] >= 7``; e.g. src/picotron/nn/triton_kernels/rmsnorm.py:140-145).
 Each op passes its own ``*Unavailable`` exception type, so callers keep catching what the
 reference raised.
 """
