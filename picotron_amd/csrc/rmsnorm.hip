@@ -11,7 +11,7 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __r
                                                                 int64_t nparts, int cols,
                                                                 void* __restrict__ dw, int wdt) {
   constexpr int kGroups = 256 / kFinishCols;
-  constexpr int kUnroll = 16;
+  constexpr int kUnroll = 64;
   __shared__ float lds[kGroups][kFinishCols + 1];
   const int col = threadIdx.x % kFinishCols;
   const int grp = threadIdx.x / kFinishCols;

@@ -93,6 +93,47 @@ __device__ __forceinline__ void load_lane_weights(const void* w, int wdt, int rl
   }
 }
 
+// A lane's weights kept as loaded and converted to fp32 at each use, which halves their
+// registers for 16-bit weights.  Vector path: 16-byte words, branch-free (a vector past the
+// row end loads the row's first weights; its products are never stored or summed).
+// Element path (runtime weight type): fp32 values, zero past the row end.
+template <typename WT, int VPL, int N, bool VECTOR>
+struct LaneWeights {
+  float f[VPL][N];
+  __device__ __forceinline__ void load(const void* w, int wdt, int rl, int lanes, int cols) {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int e = (rl + k * lanes) * N;
+      load_weight<WT, N, false>(w, wdt, e, cols - e, f[k]);
+    }
+  }
+  __device__ __forceinline__ float at(int k, int i) const { return f[k][i]; }
+};
+
+template <typename WT, int VPL, int N>
+struct LaneWeights<WT, VPL, N, true> {
+  static constexpr int kPer = 16 / static_cast<int>(sizeof(WT));  // weights per 16-byte word
+  static constexpr int kWords = N / kPer;
+  static_assert(kWords * kPer == N, "weights of one vector fill whole 16-byte words");
+  union Word {
+    u32x4 raw;
+    WT e[kPer];
+  };
+  Word wd[VPL][kWords];
+  __device__ __forceinline__ void load(const void* w, int, int rl, int lanes, int cols) {
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+      const int e = (rl + k * lanes) * N;
+      const WT* p = reinterpret_cast<const WT*>(w) + (e < cols ? e : 0);
+#pragma unroll
+      for (int l = 0; l < kWords; ++l) wd[k][l].raw = *reinterpret_cast<const u32x4*>(p + l * kPer);
+    }
+  }
+  __device__ __forceinline__ float at(int k, int i) const {
+    return static_cast<float>(wd[k][i / kPer].e[i % kPer]);
+  }
+};
+
 // The 16-byte vectors of one row held by a lane, packed in the storage type.
 template <typename T, int VPL>
 struct RowRegs {
@@ -177,10 +218,11 @@ __device__ __forceinline__ float row_sum(float v, float* red, int wave, int lane
 // compact window of rows (DRAM-friendly, like a non-persistent grid).  With a grid that
 // covers every row once (the default) each wave handles one row; smaller grids loop, and
 // the next row is then loaded into the second register buffer before the current one is
-// reduced.  Weights are loaded once per wave.
+// reduced (PERSIST).  Weights are loaded once per wave, kept packed.  Without PERSIST the
+// kernel holds one row buffer only: fewer registers, more waves in flight per CU.
 
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT>
+          bool STORE_NT, bool PERSIST>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     const T* __restrict__ x, int64_t xs, const void* __restrict__ w, int wdt, T* __restrict__ y,
     int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps, int iters) {
@@ -199,8 +241,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
   const int64_t r1 = rows;
   const float inv_cols = 1.0f / static_cast<float>(cols);
 
-  float wv[VPL][V];
-  load_lane_weights<WT, VPL, V, ALIGNED>(w, wdt, rl, LANES, cols, wv);
+  LaneWeights<WT, VPL, V, ALIGNED> wv;
+  wv.load(w, wdt, rl, LANES, cols);
 
   auto process = [&](RowRegs<T, VPL>& xr, int64_t row, int buf) {
     const bool active = row < r1;
@@ -227,7 +269,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     for (int k = 0; k < VPL; ++k) {
       float o[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) o[i] = (xr.at(k, i) * r) * wv[k][i];
+      for (int i = 0; i < V; ++i) o[i] = (xr.at(k, i) * r) * wv.at(k, i);
       store_vec<T, LANES, ALIGNED, STORE_NT>(yr, rl, k, cols, o);
     }
   };
@@ -237,17 +279,23 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
   auto load = [&](RowRegs<T, VPL>& xr, int64_t row) {
     load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + (row < r1 ? row : r1 - 1) * xs, rl, cols, xr);
   };
-  RowRegs<T, VPL> a, b;
   int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
-  load(a, ra);
-  for (int it = 0; it < iters; it += 2) {
-    const int64_t rb = ra + group_stride;
-    if (it + 1 < iters) load(b, rb);
+  if constexpr (!PERSIST) {
+    RowRegs<T, VPL> a;
+    load(a, ra);
     process(a, ra, 0);
-    const int64_t rc = rb + group_stride;
-    if (it + 2 < iters) load(a, rc);
-    if (it + 1 < iters) process(b, rb, 1);
-    ra = rc;
+  } else {
+    RowRegs<T, VPL> a, b;
+    load(a, ra);
+    for (int it = 0; it < iters; it += 2) {
+      const int64_t rb = ra + group_stride;
+      if (it + 1 < iters) load(b, rb);
+      process(a, ra, 0);
+      const int64_t rc = rb + group_stride;
+      if (it + 2 < iters) load(a, rc);
+      if (it + 1 < iters) process(b, rb, 1);
+      ra = rc;
+    }
   }
 }
 
@@ -421,7 +469,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
 
 // dW[c] = sum_p partial[p][c] in a fixed order, cast to the weight type.  A block covers
 // kFinishCols columns with 8 groups of 32 lanes; group g sums p = g, g+8, ... in increasing
-// p (16 loads in flight per lane), then the groups are added in group order.
+// p (up to 64 loads in flight per lane: one round trip at 512 partials), then the groups
+// are added in group order.
 constexpr int kFinishCols = 32;
 __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
                                                                 int64_t nparts, int cols,
@@ -595,10 +644,20 @@ struct FwdLaunch {
   template <int VPL, int WPR>
   void run() const {
     constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
-    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT>),
-                       dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
-                       static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys,
-                       a.rstd, a.rows, a.cols, a.eps, row_iters(a.rows, a.blocks, WAVES / WPR));
+    const int iters = row_iters(a.rows, a.blocks, WAVES / WPR);
+    if (iters == 1) {
+      hipLaunchKernelGGL(
+          (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>),
+          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
+          static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd,
+          a.rows, a.cols, a.eps, iters);
+    } else {
+      hipLaunchKernelGGL(
+          (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>),
+          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
+          static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd,
+          a.rows, a.cols, a.eps, iters);
+    }
   }
 };
 
