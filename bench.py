@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|adamw|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|ce_train|adamw|copy]
 
 Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
 (8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
@@ -105,6 +105,11 @@ class Workload:
 
     def cpu_baseline(self) -> dict:
         raise NotImplementedError
+
+    def extra(self, steps: int) -> dict | None:
+        """Additional figures measured after the timed passes (reported under config)."""
+
+        return None
 
 
 class RMSNormWorkload(Workload):
@@ -380,6 +385,92 @@ class CrossEntropyWorkload(Workload):
         )
 
 
+class CrossEntropyTrainWorkload(Workload):
+    """The train loop's loss and its backward through autograd on the model's whole
+    (B, S, V) logits, with the shift inside the kernel (reference call:
+    src/picotron/training/train_loop.py:141-144)."""
+
+    name = "ce_train"
+    metric = "Next-token cross-entropy fwd + autograd bwd HBM GB/s & % of peak, logits [4, 2049, 128256] bf16"
+    b, s, vocab = 4, 2049, 128256
+
+    def __init__(self, layers: int) -> None:
+        from picotron_amd.nn.triton_kernels import triton_cross_entropy
+
+        self.layers = 1
+        b, s, v = self.b, self.s, self.vocab
+        self.fn = triton_cross_entropy
+        self.leaf = _seeded((b, s, v), torch.bfloat16, 110, 2.0).requires_grad_(True)
+        g = torch.Generator(device="cuda").manual_seed(111)
+        self.ids = torch.randint(0, v, (b, s), generator=g, device="cuda")
+        flat = self.ids[:, 1:].reshape(-1)
+        flat[torch.randperm(flat.numel(), generator=g, device="cuda")[: flat.numel() // 20]] = -100
+        self.ids[:, 1:] = flat.view(b, s - 1)
+        rows = b * s
+        self.bytes_per_step = 2 * rows * v * 2 + 16 * rows
+        self.tokens_per_step = b * (s - 1)
+        self.dominant = ("shifted cross-entropy forward + autograd backward (ce_prepare_kernel + ce_rows_kernel "
+                         "+ ce_finish_kernel; the backward's ce_scale_kernel returns at once for grad 1)")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            f"train-loop loss on model logits [{b}, {s}, {v}] bf16 ~N(0,2^2) against input_ids[:, 1:] "
+            f"(5% = -100): triton_cross_entropy(logits, input_ids, shift=True) then torch.autograd.grad "
+            f"to the logits' leaf; the gradient is written into the logits buffer"
+        )
+
+    def _step(self, shifted: bool):
+        logits = self.leaf.view(self.b, self.s, self.vocab)
+        if shifted:
+            loss = self.fn(logits, self.ids, shift=True)
+        else:
+            loss = self.fn(logits[:, :-1, :].transpose(1, 2), self.ids[:, 1:])
+        # to the leaf: the view's backward is a reshape (the logits themselves are a view,
+        # whose autograd node is regenerated once the in-place gradient bumps its version)
+        (grad,) = torch.autograd.grad(loss, self.leaf)
+        return grad
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        self._step(True)
+        if events is not None:
+            end.record()
+
+    def extra(self, steps: int) -> dict:
+        """The same loss through the reference's call shape (sliced, transposed view), whose
+        backward adds autograd's slice backward: a zero-filled full-size gradient plus a copy."""
+
+        for _ in range(2):
+            self._step(False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self._step(False)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        return {"sliced_view_call_ms_per_step": round(ms, 4)}
+
+    def cpu_baseline(self) -> dict:
+        from oracle import cross_entropy as o_ce
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        s = 257
+        logits = self.leaf.detach()[:, :s].cpu()
+        ids = self.ids[:, :s].cpu()
+        sec, calls = _time_cpu(lambda: o_ce.fallback_forward_backward(
+            logits[:, :-1, :].transpose(1, 2), ids[:, 1:]))
+        rows = self.b * s
+        return dict(
+            value=(2 * rows * self.vocab * 2 + 16 * rows) / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"first {s} positions of each sequence: F.cross_entropy fwd + autograd bwd on the fp32 "
+                   f"upcast of the sliced view (the reference fallback under autocast), median of {calls} "
+                   f"calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=self.b * (s - 1) / sec,
+        )
+
+
 class AdamWWorkload(Workload):
     name = "adamw"
     metric = "Fused AdamW step HBM GB/s & % of peak, 1.2e9 fp32 params"
@@ -475,11 +566,12 @@ WORKLOADS = {
     "swiglu": SwiGLUWorkload,
     "rope": RoPEWorkload,
     "ce": CrossEntropyWorkload,
+    "ce_train": CrossEntropyTrainWorkload,
     "adamw": AdamWWorkload,
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "adamw": 1, "copy": 4}
+DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "copy": 4}
 
 
 def _traffic(workload: str) -> dict | None:
@@ -535,7 +627,8 @@ def main() -> int:
     # Pass 2 (the roofline): the same K steps again with a HIP event pair around every
     # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
     # records add a few microseconds per launch, so this pass is not used for the value.
-    per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "adamw": 1, "copy": layers}[args.workload]
+    per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
+                "copy": layers}[args.workload]
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps * per_step)]
     pending = list(reversed(events))
@@ -570,6 +663,8 @@ def main() -> int:
     if traffic:
         roofline["traffic_source"] = traffic.get("source")
 
+    extra = wl.extra(args.steps)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = wl.cpu_baseline()
@@ -601,6 +696,7 @@ def main() -> int:
             "tokens_per_s": round(wl.tokens_per_step / (elapsed / args.steps), 1),
             "layers_per_step": layers,
             "parallelism": "single GPU",
+            **(extra or {}),
         },
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -146,6 +146,30 @@ int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
                                 int64_t t_inner_stride, int64_t ignore_index,
                                 const float* grad_output, int dtype, void* stream);
 
+/* Next-token cross-entropy on the whole (batch, seq, vocab) logits of a language model:
+ * row (b, t) with t < seq-1 has target input_ids[b*ids_batch_stride + (t+1)*ids_seq_stride];
+ * the rows of the last position t = seq-1 have no target (loss 0, not counted in n_valid,
+ * gradient 0).  The loss equals pt_cross_entropy on the view
+ * logits[:, :-1, :].transpose(1, 2) with targets input_ids[:, 1:] -- the train loop's call
+ * at src/picotron/training/train_loop.py:141-144 -- but with write_grad the gradient
+ * covers the whole (batch, seq, vocab) buffer, so autograd needs no slice backward (which
+ * allocates, zero-fills and copies a full-size gradient).  Row (b, t) starts at
+ * logits + b*batch_stride + t*seq_stride.  Workspace:
+ * pt_cross_entropy_workspace_bytes(batch * seq). */
+int pt_cross_entropy_shifted(void* logits, int64_t batch, int64_t seq, int64_t batch_stride,
+                             int64_t seq_stride, int64_t vocab, const int64_t* input_ids,
+                             int64_t ids_batch_stride, int64_t ids_seq_stride,
+                             int64_t ignore_index, float* loss_out, int write_grad,
+                             void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/* pt_cross_entropy_scale_grad for a gradient written by pt_cross_entropy_shifted (same
+ * description); the last position and ignored rows stay zero. */
+int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq,
+                                        int64_t batch_stride, int64_t seq_stride, int64_t vocab,
+                                        const int64_t* input_ids, int64_t ids_batch_stride,
+                                        int64_t ids_seq_stride, int64_t ignore_index,
+                                        const float* grad_output, int dtype, void* stream);
+
 /* ---------------------------------------------------------------- AdamW
  * One decoupled-weight-decay Adam step over many fp32 tensors in one launch, with
  * torch.optim.AdamW's single-tensor arithmetic (amsgrad=False, maximize=False), per element:

@@ -49,3 +49,20 @@ def fallback_forward_backward(logits: Tensor, targets: Tensor) -> tuple[Tensor, 
     loss = torch.nn.functional.cross_entropy(lf, targets)
     loss.backward()
     return loss.detach(), lf.grad
+
+
+def shifted_forward_backward(
+    logits: Tensor, input_ids: Tensor, ignore_index: int = -100, compute: torch.dtype = torch.float64
+) -> tuple[Tensor, Tensor]:
+    """The train loop's next-token loss on (B, S, V) logits (reference
+    src/picotron/training/train_loop.py:141-144: ``logits[:, :-1, :].transpose(1, 2)``
+    against ``input_ids[:, 1:]``) and its gradient with respect to the whole logits: the
+    view's gradient in positions 0..S-2 and zero in the last position (the slice's
+    backward)."""
+
+    loss, grad_view = forward_backward(
+        logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:], ignore_index, compute
+    )
+    grad = torch.zeros(logits.shape, dtype=compute, device=logits.device)
+    grad[:, :-1, :] = grad_view.transpose(1, 2)
+    return loss, grad

@@ -67,6 +67,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
          c_int64, c_void_p, c_int, c_void_p],
     ),
+    "pt_cross_entropy_shifted": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
+         c_int64, c_void_p, c_int, c_void_p, c_size_t, c_int, c_void_p],
+    ),
+    "pt_cross_entropy_shifted_scale_grad": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
+         c_int64, c_void_p, c_int, c_void_p],
+    ),
     "pt_adamw_block_elems": (c_int64, []),
     "pt_adamw_step": (
         c_int,

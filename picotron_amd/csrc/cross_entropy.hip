@@ -79,16 +79,16 @@ __device__ __forceinline__ float block_reduce_sum(float v, float* red) {
 }
 
 __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __restrict__ targets,
-                                                               int64_t inner, int64_t tos,
-                                                               int64_t tis, int64_t rows,
-                                                               int64_t ignore_index,
+                                                               int64_t inner, int64_t valid_inner,
+                                                               int64_t tos, int64_t tis,
+                                                               int64_t rows, int64_t ignore_index,
                                                                CeWork* __restrict__ ws,
                                                                float* __restrict__ loss_out) {
   __shared__ float red[kWaves];
   float cnt = 0.0f;
   for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
     const int64_t o = r / inner, i = r - (r / inner) * inner;
-    cnt += (targets[o * tos + i * tis] != ignore_index) ? 1.0f : 0.0f;
+    if (i < valid_inner) cnt += (targets[o * tos + i * tis] != ignore_index) ? 1.0f : 0.0f;
   }
   const float total = block_reduce_sum(cnt, red);
   if (threadIdx.x == 0) {
@@ -98,21 +98,22 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
   }
 }
 
-// Common start of both row kernels: locates the row and its target.  An ignored row gets a
-// zero gradient and a zero loss, and the function returns false.  Otherwise thread 0 reads
+// Common start of both row kernels: locates the row and its target.  An ignored row (target
+// == ignore_index, or a position i >= valid_inner that has no target) gets a zero gradient
+// and a zero loss, and the function returns false.  Otherwise thread 0 reads
 // the target logit into *s_target_logit (NaN for a target outside [0, vocab), which also
 // sets status bit 0) before any thread of the block can overwrite the row: the block
 // passes at least two barriers before its first gradient store.
 template <typename T, int V, bool ALIGNED>
-__device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t os, int64_t is,
-                                             int vocab, const int64_t* targets, int64_t tos,
-                                             int64_t tis, int64_t ignore_index, int write_grad,
-                                             CeWork* ws, T** p_out, int* tgt_out,
-                                             float* s_target_logit) {
+__device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t valid_inner,
+                                             int64_t os, int64_t is, int vocab,
+                                             const int64_t* targets, int64_t tos, int64_t tis,
+                                             int64_t ignore_index, int write_grad, CeWork* ws,
+                                             T** p_out, int* tgt_out, float* s_target_logit) {
   const int64_t row = blockIdx.x;
   const int64_t o = row / inner, ii = row - (row / inner) * inner;
   T* p = logits + o * os + ii * is;
-  const int64_t tgt = targets[o * tos + ii * tis];
+  const int64_t tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
   if (tgt == ignore_index) {
     if (write_grad) {
       for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
@@ -157,16 +158,16 @@ constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
 
 template <typename T, int VPT>
 __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t os, int64_t is, int vocab,
-    const int64_t* __restrict__ targets, int64_t tos, int64_t tis, int64_t ignore_index,
-    int write_grad, CeWork* __restrict__ ws) {
+    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
+    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
   __shared__ float red[kWaves];
   __shared__ float s_target_logit;
   T* p = nullptr;
   int tgt = 0;
-  if (!ce_row_begin<T, V, true>(logits, inner, os, is, vocab, targets, tos, tis, ignore_index,
-                                write_grad, ws, &p, &tgt, &s_target_logit))
+  if (!ce_row_begin<T, V, true>(logits, inner, valid_inner, os, is, vocab, targets, tos, tis,
+                                ignore_index, write_grad, ws, &p, &tgt, &s_target_logit))
     return;
 
   Vec16<T> v[VPT];
@@ -228,16 +229,17 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
 // gradient.
 template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t os, int64_t is, int vocab,
-    const int64_t* __restrict__ targets, int64_t tos, int64_t tis, int64_t ignore_index,
-    int write_grad, CeWork* __restrict__ ws) {
+    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
+    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = ALIGNED ? Elem<T>::VEC : 1;
   __shared__ float red[kWaves];
   __shared__ float s_target_logit;
   T* p = nullptr;
   int tgt = 0;
-  if (!ce_row_begin<T, V, ALIGNED>(logits, inner, os, is, vocab, targets, tos, tis,
-                                   ignore_index, write_grad, ws, &p, &tgt, &s_target_logit))
+  if (!ce_row_begin<T, V, ALIGNED>(logits, inner, valid_inner, os, is, vocab, targets, tos,
+                                   tis, ignore_index, write_grad, ws, &p, &tgt,
+                                   &s_target_logit))
     return;
 
   auto load = [&](int e, float(&x)[V]) {
@@ -304,55 +306,76 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
 
 // In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1.
 // Ignored rows stay zero whatever the scalar is (torch's nll_loss backward leaves them 0).
-// Block b scales elements [c*kScaleChunk, (c+1)*kScaleChunk) of row b / chunks.
-constexpr int kScaleChunk = 256 * 8;
+// The work items are (row, chunk of 1024 vectors or elements); a grid of a few blocks per CU
+// walks them, so the common grad_output == 1 case costs one small launch.  ALIGNED rows
+// move 16-byte vectors (4 per thread per chunk), otherwise single elements.
+constexpr int kScaleVecs = 4;
 
-template <typename T>
+template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, int64_t inner,
-                                                       int64_t os, int64_t is, int vocab,
+                                                       int64_t valid_inner, int64_t os,
+                                                       int64_t is, int vocab, int64_t items,
                                                        int64_t chunks,
                                                        const int64_t* __restrict__ targets,
                                                        int64_t tos, int64_t tis,
                                                        int64_t ignore_index,
                                                        const float* __restrict__ scale) {
+  constexpr int V = ALIGNED ? Elem<T>::VEC : 1;
+  constexpr int kChunk = 256 * V * kScaleVecs;
   const float sc = *scale;
   if (sc == 1.0f) return;
-  const int64_t row = blockIdx.x / chunks;
-  const int64_t c = blockIdx.x - row * chunks;
-  const int64_t o = row / inner, ii = row - (row / inner) * inner;
-  if (targets[o * tos + ii * tis] == ignore_index) return;
-  T* p = logits + o * os + ii * is;
-  const int64_t e0 = c * kScaleChunk;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int64_t row = item / chunks;
+    const int64_t c = item - row * chunks;
+    const int64_t o = row / inner, ii = row - (row / inner) * inner;
+    if (ii >= valid_inner || targets[o * tos + ii * tis] == ignore_index) continue;
+    T* p = logits + o * os + ii * is;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int64_t e = e0 + k * 256 + threadIdx.x;
-    if (e < vocab) p[e] = Elem<T>::from_f32(Elem<T>::to_f32(p[e]) * sc);
+    for (int k = 0; k < kScaleVecs; ++k) {
+      const int64_t e = c * kChunk + (static_cast<int64_t>(k) * 256 + threadIdx.x) * V;
+      if (e < vocab) {
+        if constexpr (ALIGNED) {
+          float x[V];
+          load_f32<T, true>(p + e, x, V);
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[i] *= sc;
+          store_f32<T, true>(p + e, x, V);
+        } else {
+          p[e] = Elem<T>::from_f32(Elem<T>::to_f32(p[e]) * sc);
+        }
+      }
+    }
   }
 }
 
+// Row and target description shared by the launches of one call.
+struct CeRows {
+  void* logits;
+  int64_t inner, valid_inner, os, is;
+  int vocab;
+  const int64_t* targets;
+  int64_t tos, tis, ignore_index;
+};
+
 template <typename T, int VPT>
-void launch_rows(void* logits, int64_t inner, int64_t os, int64_t is, int vocab,
-                 const int64_t* targets, int64_t tos, int64_t tis, int64_t ignore_index,
-                 int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
+void launch_rows(const CeRows& d, int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
   hipLaunchKernelGGL((ce_rows_kernel<T, VPT>), dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                     0, st, static_cast<T*>(logits), inner, os, is, vocab, targets, tos, tis,
-                     ignore_index, write_grad, ws);
+                     0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is,
+                     d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
 }
 
 // Register-resident rows for up to 16 vectors per thread (131072 fp16/bf16 or 65536 fp32
 // elements); longer or unaligned rows stream.
 template <typename T>
-void dispatch_rows(bool aligned, void* logits, int64_t inner, int64_t os, int64_t is, int vocab,
-                   const int64_t* targets, int64_t tos, int64_t tis, int64_t ignore_index,
-                   int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
-  const int64_t per_thread = (static_cast<int64_t>(vocab) + int64_t{kThreads} * Elem<T>::VEC - 1) /
+void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, int64_t rows,
+                   hipStream_t st) {
+  const int64_t per_thread = (static_cast<int64_t>(d.vocab) + int64_t{kThreads} * Elem<T>::VEC - 1) /
                              (int64_t{kThreads} * Elem<T>::VEC);
   if (aligned) {
-#define PT_CE_CASE(N)                                                                        \
-  if (per_thread <= N) {                                                                     \
-    launch_rows<T, N>(logits, inner, os, is, vocab, targets, tos, tis, ignore_index,         \
-                      write_grad, ws, rows, st);                                             \
-    return;                                                                                  \
+#define PT_CE_CASE(N)                                  \
+  if (per_thread <= N) {                               \
+    launch_rows<T, N>(d, write_grad, ws, rows, st);    \
+    return;                                            \
   }
     PT_CE_CASE(1)
     PT_CE_CASE(2)
@@ -361,13 +384,101 @@ void dispatch_rows(bool aligned, void* logits, int64_t inner, int64_t os, int64_
     PT_CE_CASE(16)
 #undef PT_CE_CASE
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
-                       dim3(kThreads), 0, st, static_cast<T*>(logits), inner, os, is, vocab,
-                       targets, tos, tis, ignore_index, write_grad, ws);
+                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
+                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
+                       ws);
   } else {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, false>), dim3(static_cast<unsigned>(rows)),
-                       dim3(kThreads), 0, st, static_cast<T*>(logits), inner, os, is, vocab,
-                       targets, tos, tis, ignore_index, write_grad, ws);
+                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
+                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
+                       ws);
   }
+}
+
+// The fused loss over outer x inner rows, of which positions i >= valid_inner carry no target.
+int ce_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_t vocab,
+           float* loss_out, int write_grad, void* workspace, size_t workspace_bytes, int dtype,
+           void* stream) {
+  const std::string name(fn);
+  if (!valid_dtype(dtype)) return fail(PT_EINVAL, name + ": unknown dtype code");
+  if (outer < 0 || inner < 0 || vocab <= 0) return fail(PT_EINVAL, name + ": bad shape");
+  if (vocab > (int64_t{1} << 30)) return fail(PT_EUNSUPPORTED, name + ": vocab too large");
+  const int64_t rows = outer * inner;
+  // One 1024-thread workgroup per row; an HSA grid holds at most 2^32 - 1 work-items.
+  if (rows * kThreads > 0xffffffffLL)
+    return fail(PT_EUNSUPPORTED, name + ": more than 4194303 rows");
+  if (!loss_out || !workspace) return fail(PT_EINVAL, name + ": null pointer");
+  if (rows > 0 && (!d.logits || (d.valid_inner > 0 && !d.targets)))
+    return fail(PT_EINVAL, name + ": null pointer");
+  if (workspace_bytes < pt_cross_entropy_workspace_bytes(rows) || !aligned16(workspace))
+    return fail(PT_EINVAL, name + ": workspace too small or not 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  CeWork* ws = static_cast<CeWork*>(workspace);
+  hipLaunchKernelGGL(ce_prepare_kernel, dim3(1), dim3(kThreads), 0, st, d.targets, d.inner,
+                     d.valid_inner, d.tos, d.tis, rows, d.ignore_index, ws, loss_out);
+  if (int rc = check_launch(fn)) return rc;
+  if (rows == 0) return ok();
+  const int esize = dtype_size(dtype);
+  const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
+                       (outer <= 1 || (d.os * esize) % 16 == 0) &&
+                       (inner <= 1 || (d.is * esize) % 16 == 0);
+  if (dtype == PT_FLOAT32) {
+    dispatch_rows<float>(aligned, d, write_grad, ws, rows, st);
+  } else if (dtype == PT_FLOAT16) {
+    dispatch_rows<_Float16>(aligned, d, write_grad, ws, rows, st);
+  } else {
+    dispatch_rows<__bf16>(aligned, d, write_grad, ws, rows, st);
+  }
+  if (int rc = check_launch(fn)) return rc;
+  hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(kThreads), 0, st, ws, rows, loss_out);
+  return check_launch(fn);
+}
+
+template <typename T, bool ALIGNED>
+void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, hipStream_t st) {
+  constexpr int64_t kChunk = 256 * (ALIGNED ? Elem<T>::VEC : 1) * kScaleVecs;
+  const int64_t chunks = (d.vocab + kChunk - 1) / kChunk;
+  const int64_t items = rows * chunks;
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
+  const unsigned grid = static_cast<unsigned>(items < cap ? items : cap);
+  hipLaunchKernelGGL((ce_scale_kernel<T, ALIGNED>), dim3(grid), dim3(256), 0, st,
+                     static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is, d.vocab, items,
+                     chunks, d.targets, d.tos, d.tis, d.ignore_index, grad_output);
+}
+
+template <typename T>
+void scale_launch(bool aligned, const CeRows& d, int64_t rows, const float* grad_output,
+                  hipStream_t st) {
+  if (aligned) {
+    scale_launch_as<T, true>(d, rows, grad_output, st);
+  } else {
+    scale_launch_as<T, false>(d, rows, grad_output, st);
+  }
+}
+
+int ce_scale_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_t vocab,
+                 const float* grad_output, int dtype, void* stream) {
+  const std::string name(fn);
+  if (!valid_dtype(dtype)) return fail(PT_EINVAL, name + ": unknown dtype");
+  if (outer < 0 || inner < 0 || vocab <= 0 || vocab > (int64_t{1} << 30))
+    return fail(PT_EINVAL, name + ": bad shape");
+  const int64_t rows = outer * inner;
+  if (rows == 0) return ok();
+  if (!d.logits || (d.valid_inner > 0 && !d.targets) || !grad_output)
+    return fail(PT_EINVAL, name + ": null pointer");
+  hipStream_t st = as_stream(stream);
+  const int esize = dtype_size(dtype);
+  const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
+                       (outer <= 1 || (d.os * esize) % 16 == 0) &&
+                       (inner <= 1 || (d.is * esize) % 16 == 0);
+  if (dtype == PT_FLOAT32) {
+    scale_launch<float>(aligned, d, rows, grad_output, st);
+  } else if (dtype == PT_FLOAT16) {
+    scale_launch<_Float16>(aligned, d, rows, grad_output, st);
+  } else {
+    scale_launch<__bf16>(aligned, d, rows, grad_output, st);
+  }
+  return check_launch(fn);
 }
 
 }  // namespace
@@ -391,44 +502,12 @@ int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_s
                      int64_t t_outer_stride, int64_t t_inner_stride, int64_t ignore_index,
                      float* loss_out, int write_grad, void* workspace, size_t workspace_bytes,
                      int dtype, void* stream) {
-  if (!valid_dtype(dtype)) return fail(PT_EINVAL, "pt_cross_entropy: unknown dtype code");
-  if (outer < 0 || inner < 0 || vocab <= 0)
-    return fail(PT_EINVAL, "pt_cross_entropy: bad shape");
-  if (vocab > (int64_t{1} << 30)) return fail(PT_EUNSUPPORTED, "pt_cross_entropy: vocab too large");
-  const int64_t rows = outer * inner;
-  // One 1024-thread workgroup per row; an HSA grid holds at most 2^32 - 1 work-items.
-  if (rows * kThreads > 0xffffffffLL)
-    return fail(PT_EUNSUPPORTED, "pt_cross_entropy: more than 4194303 rows");
-  if (!loss_out || !workspace) return fail(PT_EINVAL, "pt_cross_entropy: null pointer");
-  if (rows > 0 && (!logits || !targets)) return fail(PT_EINVAL, "pt_cross_entropy: null pointer");
-  if (workspace_bytes < pt_cross_entropy_workspace_bytes(rows) || !aligned16(workspace))
-    return fail(PT_EINVAL, "pt_cross_entropy: workspace too small or not 16-byte aligned");
-  hipStream_t st = as_stream(stream);
-  CeWork* ws = static_cast<CeWork*>(workspace);
   const int64_t inner_nz = inner > 0 ? inner : 1;
-  hipLaunchKernelGGL(ce_prepare_kernel, dim3(1), dim3(kThreads), 0, st, targets, inner_nz,
-                     t_outer_stride, t_inner_stride, rows, ignore_index, ws, loss_out);
-  if (int rc = check_launch("pt_cross_entropy (prepare)")) return rc;
-  if (rows == 0) return ok();
-  const int esize = dtype_size(dtype);
-  const bool aligned = aligned16(logits) && (vocab * esize) % 16 == 0 &&
-                       (outer <= 1 || (outer_stride * esize) % 16 == 0) &&
-                       (inner <= 1 || (inner_stride * esize) % 16 == 0);
-  const int v = static_cast<int>(vocab);
-  if (dtype == PT_FLOAT32) {
-    dispatch_rows<float>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
-                         t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows, st);
-  } else if (dtype == PT_FLOAT16) {
-    dispatch_rows<_Float16>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
-                            t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows,
-                            st);
-  } else {
-    dispatch_rows<__bf16>(aligned, logits, inner_nz, outer_stride, inner_stride, v, targets,
-                          t_outer_stride, t_inner_stride, ignore_index, write_grad, ws, rows, st);
-  }
-  if (int rc = check_launch("pt_cross_entropy (rows)")) return rc;
-  hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(kThreads), 0, st, ws, rows, loss_out);
-  return check_launch("pt_cross_entropy (finish)");
+  const CeRows d{logits, inner_nz, inner_nz, outer_stride, inner_stride,
+                 static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
+                 targets, t_outer_stride, t_inner_stride, ignore_index};
+  return ce_run("pt_cross_entropy", d, outer, inner, vocab, loss_out, write_grad, workspace,
+                workspace_bytes, dtype, stream);
 }
 
 int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
@@ -436,37 +515,47 @@ int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
                                 const int64_t* targets, int64_t t_outer_stride,
                                 int64_t t_inner_stride, int64_t ignore_index,
                                 const float* grad_output, int dtype, void* stream) {
-  if (!valid_dtype(dtype)) return fail(PT_EINVAL, "pt_cross_entropy_scale_grad: unknown dtype");
-  if (outer < 0 || inner < 0 || vocab <= 0 || vocab > (int64_t{1} << 30))
-    return fail(PT_EINVAL, "pt_cross_entropy_scale_grad: bad shape");
-  const int64_t rows = outer * inner;
-  if (rows == 0) return ok();
-  if (!logits || !targets || !grad_output)
-    return fail(PT_EINVAL, "pt_cross_entropy_scale_grad: null pointer");
-  const int64_t chunks = (vocab + kScaleChunk - 1) / kScaleChunk;
-  const int64_t blocks = rows * chunks;
-  if (blocks * 256 > 0xffffffffLL)
-    return fail(PT_EUNSUPPORTED, "pt_cross_entropy_scale_grad: grid too large");
-  hipStream_t st = as_stream(stream);
-  const int v = static_cast<int>(vocab);
   const int64_t inner_nz = inner > 0 ? inner : 1;
-  if (dtype == PT_FLOAT32) {
-    hipLaunchKernelGGL(ce_scale_kernel<float>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       st, static_cast<float*>(logits), inner_nz, outer_stride, inner_stride, v,
-                       chunks, targets, t_outer_stride, t_inner_stride, ignore_index,
-                       grad_output);
-  } else if (dtype == PT_FLOAT16) {
-    hipLaunchKernelGGL(ce_scale_kernel<_Float16>, dim3(static_cast<unsigned>(blocks)), dim3(256),
-                       0, st, static_cast<_Float16*>(logits), inner_nz, outer_stride,
-                       inner_stride, v, chunks, targets, t_outer_stride, t_inner_stride,
-                       ignore_index, grad_output);
-  } else {
-    hipLaunchKernelGGL(ce_scale_kernel<__bf16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       st, static_cast<__bf16*>(logits), inner_nz, outer_stride, inner_stride, v,
-                       chunks, targets, t_outer_stride, t_inner_stride, ignore_index,
-                       grad_output);
-  }
-  return check_launch("pt_cross_entropy_scale_grad");
+  const CeRows d{logits, inner_nz, inner_nz, outer_stride, inner_stride,
+                 static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
+                 targets, t_outer_stride, t_inner_stride, ignore_index};
+  return ce_scale_run("pt_cross_entropy_scale_grad", d, outer, inner, vocab, grad_output, dtype,
+                      stream);
+}
+
+// Rows (b, t) of (batch, seq, vocab) logits; row t < seq - 1 predicts input_ids[b, t + 1], so
+// the targets start one position into input_ids and the last position has none.
+static CeRows shifted_rows(void* logits, int64_t seq, int64_t batch_stride, int64_t seq_stride,
+                           int64_t vocab, const int64_t* input_ids, int64_t ids_batch_stride,
+                           int64_t ids_seq_stride, int64_t ignore_index) {
+  const int64_t inner_nz = seq > 0 ? seq : 1;
+  const int64_t valid = seq > 1 ? seq - 1 : 0;
+  const int64_t* targets = (input_ids != nullptr && valid > 0) ? input_ids + ids_seq_stride : nullptr;
+  return CeRows{logits, inner_nz, valid, batch_stride, seq_stride,
+                static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
+                targets, ids_batch_stride, ids_seq_stride, ignore_index};
+}
+
+int pt_cross_entropy_shifted(void* logits, int64_t batch, int64_t seq, int64_t batch_stride,
+                             int64_t seq_stride, int64_t vocab, const int64_t* input_ids,
+                             int64_t ids_batch_stride, int64_t ids_seq_stride,
+                             int64_t ignore_index, float* loss_out, int write_grad,
+                             void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+  const CeRows d = shifted_rows(logits, seq, batch_stride, seq_stride, vocab, input_ids,
+                                ids_batch_stride, ids_seq_stride, ignore_index);
+  return ce_run("pt_cross_entropy_shifted", d, batch, seq, vocab, loss_out, write_grad,
+                workspace, workspace_bytes, dtype, stream);
+}
+
+int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq,
+                                        int64_t batch_stride, int64_t seq_stride, int64_t vocab,
+                                        const int64_t* input_ids, int64_t ids_batch_stride,
+                                        int64_t ids_seq_stride, int64_t ignore_index,
+                                        const float* grad_output, int dtype, void* stream) {
+  const CeRows d = shifted_rows(logits, seq, batch_stride, seq_stride, vocab, input_ids,
+                                ids_batch_stride, ids_seq_stride, ignore_index);
+  return ce_scale_run("pt_cross_entropy_shifted_scale_grad", d, batch, seq, vocab, grad_output,
+                      dtype, stream);
 }
 
 }  // extern "C"

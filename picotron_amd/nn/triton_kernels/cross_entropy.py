@@ -13,6 +13,12 @@ In-place contract: after a grad-enabled call the logits tensor holds the gradien
 the logits.  Its autograd version counter is bumped, so any other graph node that saved
 those logits fails loudly at backward instead of reading wrong values.  Pass
 ``inplace=False`` to keep the logits (the gradient then goes to a copy).
+
+``shift=True`` takes the language model's whole (B, S, V) logits and the (B, S) input ids
+and computes the train loop's next-token loss (reference
+src/picotron/training/train_loop.py:141-144, ``logits[:, :-1, :].transpose(1, 2)`` against
+``input_ids[:, 1:]``) without the slice: the gradient then covers the whole logits buffer
+(last position zero), so autograd skips the slice backward's full-size zero fill and copy.
 """
 
 from __future__ import annotations
@@ -59,35 +65,76 @@ class _FusedCrossEntropy(torch.autograd.Function):
         return grad, None, None, None
 
 
-def _validate(logits: Tensor, targets: Tensor, ignore_index: int) -> None:
-    require_hip(TritonCrossEntropyUnavailable, "cross-entropy", logits, targets)
-    if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
-        raise TritonCrossEntropyUnavailable("HIP cross-entropy supports float logits only.")
-    try:
-        outer, inner, _, _, _ = ops.ce_rows(logits)
-        ops.ce_target_strides(targets, outer, inner)
-    except ValueError as error:
-        raise TritonCrossEntropyUnavailable(f"HIP cross-entropy: {error}.") from error
+class _FusedShiftedCrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits: Tensor, input_ids: Tensor, ignore_index: int, inplace: bool):  # type: ignore[override]
+        write_grad = ctx.needs_input_grad[0]
+        buffer = logits.detach()
+        if write_grad and not inplace:
+            buffer = buffer.clone()
+        loss, _ = ops.cross_entropy_shifted(buffer, input_ids, ignore_index, write_grad=write_grad)
+        if write_grad:
+            if inplace:
+                torch.autograd.graph.increment_version(logits)
+            ctx.grad_buffer = buffer
+            ctx.input_ids = input_ids
+            ctx.ignore_index = ignore_index
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss: Tensor):  # type: ignore[override]
+        grad = ctx.grad_buffer
+        ops.cross_entropy_shifted_scale_grad(grad, ctx.input_ids, grad_loss, ctx.ignore_index)
+        del ctx.grad_buffer
+        return grad, None, None, None
+
+
+def _check_targets(targets: Tensor, vocab: int, ignore_index: int) -> None:
     if os.environ.get(_CHECK_ENV, "") not in ("", "0"):
-        vocab = logits.size(1)
         bad = ((targets < 0) | (targets >= vocab)) & (targets != ignore_index)
         if bool(bad.any().item()):
             raise TritonCrossEntropyUnavailable("HIP cross-entropy targets are out of range.")
 
 
+def _validate(logits: Tensor, targets: Tensor, ignore_index: int, shift: bool) -> None:
+    require_hip(TritonCrossEntropyUnavailable, "cross-entropy", logits, targets)
+    if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise TritonCrossEntropyUnavailable("HIP cross-entropy supports float logits only.")
+    try:
+        if shift:
+            ops._shifted_desc(logits, targets)
+        else:
+            outer, inner, _, _, _ = ops.ce_rows(logits)
+            ops.ce_target_strides(targets, outer, inner)
+    except ValueError as error:
+        raise TritonCrossEntropyUnavailable(f"HIP cross-entropy: {error}.") from error
+    if shift:
+        _check_targets(targets[:, 1:], logits.size(2), ignore_index)
+    else:
+        _check_targets(targets, logits.size(1), ignore_index)
+
+
 def triton_cross_entropy(
-    logits: Tensor, targets: Tensor, *, ignore_index: int = IGNORE_INDEX, inplace: bool = True
+    logits: Tensor,
+    targets: Tensor,
+    *,
+    ignore_index: int = IGNORE_INDEX,
+    inplace: bool = True,
+    shift: bool = False,
 ) -> Tensor:
     """Mean cross-entropy over targets != ignore_index as an fp32 scalar.
 
     ``logits`` is (N, C) or (N, C, d) with a contiguous class dimension (such as the
     ``logits[:, :-1, :].transpose(1, 2)`` view of the train loop); ``targets`` is (N,) or
-    (N, d) int64.  A non-ignored target outside [0, C) gives a NaN loss (set
+    (N, d) int64.  With ``shift=True``, ``logits`` is the model's (B, S, V) output and
+    ``targets`` the (B, S) input ids: the loss is that of ``logits[:, :-1, :]`` against
+    ``targets[:, 1:]``.  A non-ignored target outside [0, C) gives a NaN loss (set
     PICOTRON_HIP_CE_CHECK=1 to raise instead, at the cost of a host sync).
     """
 
-    _validate(logits, targets, ignore_index)
-    return _FusedCrossEntropy.apply(logits, targets, int(ignore_index), bool(inplace))
+    _validate(logits, targets, ignore_index, shift)
+    fn = _FusedShiftedCrossEntropy if shift else _FusedCrossEntropy
+    return fn.apply(logits, targets, int(ignore_index), bool(inplace))
 
 
 class CrossEntropyWithFallback:
@@ -98,10 +145,14 @@ class CrossEntropyWithFallback:
         self.use_triton = use_triton
         self._fallback_warned = False
 
-    def __call__(self, logits: Tensor, targets: Tensor) -> Tensor:
+    def __call__(self, logits: Tensor, targets: Tensor, *, shift: bool = False) -> Tensor:
+        """``shift=True``: ``logits`` (B, S, V) and ``targets`` the (B, S) input ids; the
+        loss is the train loop's ``F.cross_entropy(logits[:, :-1, :].transpose(1, 2),
+        targets[:, 1:])`` (reference train_loop.py:141-144)."""
+
         if self.use_triton:
             try:
-                return triton_cross_entropy(logits, targets)
+                return triton_cross_entropy(logits, targets, shift=shift)
             except Exception as error:
                 if not self._fallback_warned:
                     warnings.warn(
@@ -110,4 +161,6 @@ class CrossEntropyWithFallback:
                         stacklevel=2,
                     )
                     self._fallback_warned = True
+        if shift:
+            return F.cross_entropy(logits[:, :-1, :].transpose(1, 2), targets[:, 1:])
         return F.cross_entropy(logits, targets)

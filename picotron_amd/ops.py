@@ -308,6 +308,57 @@ def cross_entropy_scale_grad(
     )
 
 
+def _shifted_desc(logits: Tensor, input_ids: Tensor) -> tuple[int, int, int, int, int, int, int]:
+    """(batch, seq, batch_stride, seq_stride, vocab, ids_batch_stride, ids_seq_stride)."""
+
+    if logits.dim() != 3:
+        raise ValueError("shifted cross-entropy logits must be (batch, seq, vocab)")
+    b, s, v = logits.shape
+    if logits.stride(2) != 1 and v > 1:
+        raise ValueError("cross-entropy logits need a contiguous vocabulary dimension")
+    if input_ids.dtype != torch.long:
+        raise ValueError("cross-entropy targets must be int64")
+    if input_ids.dim() != 2 or tuple(input_ids.shape) != (b, s):
+        raise ValueError("input_ids must be (batch, seq) like the logits")
+    return b, s, logits.stride(0), logits.stride(1), v, input_ids.stride(0), input_ids.stride(1)
+
+
+def cross_entropy_shifted(
+    logits: Tensor, input_ids: Tensor, ignore_index: int = -100, write_grad: bool = False
+) -> tuple[Tensor, Tensor]:
+    """Next-token mean cross-entropy of (B, S, V) logits against input_ids[:, 1:]: equal to
+    :func:`cross_entropy` on ``logits[:, :-1, :].transpose(1, 2)``.  With ``write_grad`` the
+    whole logits buffer is overwritten by d(loss)/d(logits) (last position zero)."""
+
+    device = _check_cuda(logits, input_ids)
+    b, s, bs, ss, v, ibs, iss = _shifted_desc(logits, input_ids)
+    ws_bytes = _lib.lib().pt_cross_entropy_workspace_bytes(b * s)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    loss = torch.empty((), dtype=torch.float32, device=device)
+    _lib.call(
+        "pt_cross_entropy_shifted",
+        logits.data_ptr(), b, s, bs, ss, v, input_ids.data_ptr(), ibs, iss, int(ignore_index),
+        loss.data_ptr(), int(write_grad), ws.data_ptr(), ws_bytes, dtype_code(logits.dtype),
+        _stream(device),
+    )
+    return loss, ws
+
+
+def cross_entropy_shifted_scale_grad(
+    dlogits: Tensor, input_ids: Tensor, grad_output: Tensor, ignore_index: int = -100
+) -> None:
+    """dlogits *= grad_output in place for a gradient from :func:`cross_entropy_shifted`."""
+
+    device = _check_cuda(dlogits, input_ids, grad_output)
+    b, s, bs, ss, v, ibs, iss = _shifted_desc(dlogits, input_ids)
+    go = grad_output.detach().to(torch.float32).reshape(())
+    _lib.call(
+        "pt_cross_entropy_shifted_scale_grad",
+        dlogits.data_ptr(), b, s, bs, ss, v, input_ids.data_ptr(), ibs, iss, int(ignore_index),
+        go.data_ptr(), dtype_code(dlogits.dtype), _stream(device),
+    )
+
+
 # ------------------------------------------------------------------ AdamW
 
 

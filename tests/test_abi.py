@@ -64,6 +64,10 @@ def test_workspace_queries():
         ("pt_rope", (None, None, None, None, None, None, 7, None, None, 1, 0, 0, 2, None), _lib.PT_EINVAL),
         ("pt_adamw_step", (None, 1, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
         ("pt_copy", (None, None, 16, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy", (None, 4, 1, 8, 0, 8, None, 1, 0, -100, None, 0, None, 0, 7, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 1 << 31, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EUNSUPPORTED),
+        ("pt_cross_entropy_shifted_scale_grad", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 2, None), _lib.PT_EINVAL),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(fn, args, code):
@@ -80,4 +84,5 @@ def test_empty_inputs_are_no_ops():
     assert lib.pt_swiglu_fwd(None, None, None, 0, 2, None) == _lib.PT_OK
     assert lib.pt_swiglu_bwd(None, None, None, None, None, 5, 2, None) == _lib.PT_OK
     assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
+    assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, 2, None) == _lib.PT_OK
     assert lib.pt_last_error() == b""

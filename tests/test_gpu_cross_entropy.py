@@ -171,3 +171,99 @@ def test_autograd_surface_and_grad_scaling(gpu):
     assert torch.equal(y.detach(), full)
     loss2.backward()
     _grad_close(x.grad, expected / 3.0, n_valid, torch.bfloat16)
+
+
+def _shifted_case(gpu, b, s, v, dtype, seed):
+    logits = randn((b, s, v), dtype, gpu, seed, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(seed + 1)
+    ids = torch.randint(0, v, (b, s), generator=g, device=gpu)
+    if s > 3:
+        ids[0, 2] = -100
+        ids[-1, -1] = -100
+    return logits, ids
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b,s,v", [(2, 65, 3000), (3, 17, 50257), (1, 9, 1001), (2, 2, 128)])
+def test_shifted_matches_the_train_loop_expression(gpu, dtype, b, s, v):
+    logits, ids = _shifted_case(gpu, b, s, v, dtype, 7 * s + v)
+    ref_loss, ref_grad = o_ce.shifted_forward_backward(logits, ids)
+    n_valid = int((ids[:, 1:] != -100).sum())
+    loss, ws = ops.cross_entropy_shifted(logits, ids)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    view_loss, _ = ops.cross_entropy(logits[:, :-1, :].transpose(1, 2), ids[:, 1:])
+    assert abs(loss.item() - view_loss.item()) <= 1e-6 * abs(view_loss.item())
+    buf = logits.clone()
+    loss2, ws = ops.cross_entropy_shifted(buf, ids, write_grad=True)
+    assert loss2.item() == loss.item()
+    assert ops.cross_entropy_status(ws) == 0
+    _grad_close(buf, ref_grad, n_valid, dtype)
+    assert bool((buf[:, -1, :] == 0).all())  # the last position has no target
+
+
+def test_shifted_full_config_bf16(gpu):
+    # (B, S, V) = (4, 2049, 128256) bf16: 8196 predicted positions, about the cfg5 row count
+    b, s, v = 4, 2049, 128256
+    logits, ids = _shifted_case(gpu, b, s, v, torch.bfloat16, 91)
+    ids[1, 100:300] = -100
+    n_valid = int((ids[:, 1:] != -100).sum())
+    ref_loss, ref_grad = o_ce.shifted_forward_backward(logits, ids)
+    loss, ws = ops.cross_entropy_shifted(logits, ids, write_grad=True)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    assert ops.cross_entropy_status(ws) == 0
+    _grad_close(logits, ref_grad, n_valid, torch.bfloat16)
+    del ref_grad
+    row_sums = logits.double().sum(-1) * n_valid  # kept rows of softmax - onehot sum to 0
+    assert float(row_sums.abs().max()) < 5e-3
+    assert bool((logits[:, -1, :] == 0).all())
+    assert bool((logits[1, 99:299, :] == 0).all())  # positions whose next id is ignored
+
+
+def test_shifted_single_position_has_no_targets(gpu):
+    logits = randn((3, 1, 64), torch.float32, gpu, 5)
+    ids = torch.randint(0, 64, (3, 1), device=gpu)
+    buf = logits.clone()
+    loss, _ = ops.cross_entropy_shifted(buf, ids, write_grad=True)
+    assert math.isnan(loss.item())  # mean over no targets, as F.cross_entropy
+    assert bool((buf == 0).all())
+
+
+def test_shifted_autograd_surface(gpu):
+    from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback, triton_cross_entropy
+
+    full, ids = _shifted_case(gpu, 2, 33, 500, torch.bfloat16, 83)
+    ref_loss, ref_grad = o_ce.shifted_forward_backward(full, ids)
+    n_valid = int((ids[:, 1:] != -100).sum())
+    leaf = full.clone().requires_grad_(True)
+    ce = CrossEntropyWithFallback(use_triton=True)
+    loss = ce(leaf * 1, ids, shift=True)
+    assert not ce._fallback_warned
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    (2.5 * loss).backward()  # grad_output != 1: on-device scaling, last position stays 0
+    _grad_close(leaf.grad, 2.5 * ref_grad, n_valid, torch.bfloat16)
+    assert bool((leaf.grad[:, -1, :] == 0).all())
+    x = full.clone().requires_grad_(True)
+    y = x * 1
+    loss2 = triton_cross_entropy(y, ids, shift=True, inplace=False)
+    assert torch.equal(y.detach(), full)
+    loss2.backward()
+    _grad_close(x.grad, ref_grad, n_valid, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("vocab", [512, 1001, 131072])
+def test_scale_grad(gpu, dtype, vocab):
+    # the backward's on-device scaling, for aligned (16-byte vector) and element-wise rows;
+    # ignored rows stay exactly 0 whatever the scale (NaN included)
+    rows = 9
+    logits = randn((rows, vocab), dtype, gpu, vocab + 3, 2.0)
+    targets = torch.randint(0, vocab, (rows,), device=gpu)
+    targets[4] = -100
+    _, ref_grad = o_ce.forward_backward(logits, targets)
+    buf = logits.clone()
+    ops.cross_entropy(buf, targets, write_grad=True)
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu))
+    _grad_close(buf, 0.37 * ref_grad, rows - 1, dtype)
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(float("nan"), device=gpu))
+    assert bool((buf[4] == 0).all())
+    assert bool(torch.isnan(buf[targets != -100]).all())

@@ -299,3 +299,20 @@ def test_adamw_zero_gradient_no_decay_is_identity():
     z = torch.zeros(10, dtype=torch.float64)
     p, m, v = o_adamw.step(p0, z, z, z, t=1, lr=0.1, beta1=0.9, beta2=0.99, eps=1e-8, weight_decay=0.0)
     assert torch.equal(p, p0) and torch.equal(m, z) and torch.equal(v, z)
+
+
+def test_cross_entropy_shifted_oracle_matches_torch_autograd_through_the_slice():
+    # the train loop's exact expression, differentiated by torch through slice + transpose
+    torch.manual_seed(10)
+    b, s, v = 3, 7, 29
+    logits = 2 * torch.randn(b, s, v, dtype=torch.float64)
+    ids = torch.randint(0, v, (b, s))
+    ids[1, 3] = -100
+    ids[2, 0] = -100  # position 0 is never a target: must not matter
+    lr = logits.clone().requires_grad_(True)
+    ref = F.cross_entropy(lr[:, :-1, :].transpose(1, 2), ids[:, 1:])
+    ref.backward()
+    loss, grad = o_ce.shifted_forward_backward(logits, ids)
+    torch.testing.assert_close(loss, ref.detach(), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(grad, lr.grad, rtol=1e-10, atol=1e-12)
+    assert torch.equal(grad[:, -1, :], torch.zeros(b, v, dtype=torch.float64))

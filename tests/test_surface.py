@@ -161,6 +161,19 @@ def test_triton_cross_entropy_cpu_fallback_matches_pytorch():
     assert callable(triton_cross_entropy)
 
 
+def test_shifted_cross_entropy_cpu_fallback_is_the_train_loop_expression():
+    torch.manual_seed(3)
+    logits = torch.randn(2, 5, 7)
+    ids = torch.randint(0, 7, (2, 5))
+    ids[0, 2] = -100
+    ce = CrossEntropyWithFallback(use_triton=True)
+    with pytest.warns(RuntimeWarning, match="Triton cross-entropy unavailable"):
+        actual = ce(logits, ids, shift=True)
+    torch.testing.assert_close(actual, F.cross_entropy(logits[:, :-1, :].transpose(1, 2), ids[:, 1:]))
+    plain = CrossEntropyWithFallback(use_triton=False)
+    torch.testing.assert_close(plain(logits, ids, shift=True), actual)
+
+
 def test_adamw_fallback_matches_known_single_step_update():
     parameter = torch.nn.Parameter(torch.tensor([1.0]))
     optimizer = AdamW([parameter], lr=0.1, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
