@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|ce_train|adamw|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|copy]
 
 Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
 (8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
@@ -528,6 +528,90 @@ class AdamWWorkload(Workload):
         )
 
 
+class AdamWClipWorkload(AdamWWorkload):
+    """Gradient clipping fused into the AdamW step (the train loop's
+    clip_grad_norm_ + step, src/picotron/training/train_loop.py:163-168,338-350)."""
+
+    name = "adamw_clip"
+    metric = "Fused grad-norm clip + AdamW step HBM GB/s & % of peak, 1.2e9 fp32 params"
+
+    def __init__(self, layers: int) -> None:
+        super().__init__(layers)
+        n = self.n
+        self.ws_bytes = self.lib.pt_clip_grad_norm_workspace_bytes(self.blocks)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
+        self.out = torch.empty(2, dtype=torch.float32, device="cuda")
+        self.bytes_per_step = 36 * n  # norm: read g; step: read p, g, m, v, write p, m, v, g
+        self.dominant = ("fused clip + step (grad_sumsq_kernel + grad_norm_finish_kernel + "
+                         "adamw_kernel with the clip coefficient, clipped grads written back)")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "torch.nn.utils.clip_grad_norm_(max_norm 1.0) + AdamW step fused, one flat 1.2e9-element "
+            "fp32 parameter, lr 3e-4, betas (0.9, 0.95), eps 1e-8, wd 0.1; step = norm pass + one "
+            "optimizer pass that scales each gradient by the device-side clip coefficient and writes "
+            "it back"
+        )
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        out = self.out.data_ptr()
+        rc = self.lib.pt_clip_grad_norm(_p(self.table), 1, self.blocks, 1.0, ctypes.c_void_p(out),
+                                        ctypes.c_void_p(out + 4), _p(self.ws), self.ws_bytes, self.stream)
+        if rc == 0:
+            rc = self.lib.pt_adamw_step_scaled(_p(self.table), 1, self.blocks, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                                               float(self.t), ctypes.c_void_p(out + 4), 1, self.stream)
+        if events is not None:
+            end.record()
+        self.t += 1
+        if rc:
+            _lib.check("pt_clip_grad_norm / pt_adamw_step_scaled", rc)
+
+    def extra(self, steps: int) -> dict:
+        """The unfused sequence for comparison: torch's clip_grad_norm_ (foreach norm + scale
+        pass) followed by the plain fused step."""
+
+        prm = torch.nn.Parameter(self.p)
+        prm.grad = self.g
+        def unfused():
+            torch.nn.utils.clip_grad_norm_([prm], 1.0)
+            rc = self.lib.pt_adamw_step(_p(self.table), 1, self.blocks, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                                        float(self.t), self.stream)
+            self.t += 1
+            if rc:
+                _lib.check("pt_adamw_step", rc)
+        unfused()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            unfused()
+        torch.cuda.synchronize()
+        return {"unfused_clip_then_step_ms_per_step": round((time.perf_counter() - t0) / steps * 1e3, 4)}
+
+    def cpu_baseline(self) -> dict:
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        n = 120_000_000
+        p = torch.nn.Parameter(self.p[:n].cpu())
+        g = self.g[:n].cpu()
+        opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+
+        def clip_step():
+            p.grad = g.clone()
+            torch.nn.utils.clip_grad_norm_([p], 1.0)
+            opt.step()
+
+        sec, calls = _time_cpu(clip_step)
+        return dict(
+            value=36 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"{n:.1e} of 1.2e9 params (1/10): torch.nn.utils.clip_grad_norm_ + "
+                   f"torch.optim.AdamW(foreach=False).step() on CPU (the reference train loop's "
+                   f"fallback), median of {calls} calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, params_per_s=n / sec,
+        )
+
+
 class CopyWorkload(Workload):
     name = "copy"
     metric = "128-bit streaming copy HBM GB/s (achievable-bandwidth reference)"
@@ -568,10 +652,12 @@ WORKLOADS = {
     "ce": CrossEntropyWorkload,
     "ce_train": CrossEntropyTrainWorkload,
     "adamw": AdamWWorkload,
+    "adamw_clip": AdamWClipWorkload,
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "copy": 4}
+DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
+                  "copy": 4}
 
 
 def _traffic(workload: str) -> dict | None:
@@ -628,7 +714,7 @@ def main() -> int:
     # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
     # records add a few microseconds per launch, so this pass is not used for the value.
     per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
-                "copy": layers}[args.workload]
+                "adamw_clip": 1, "copy": layers}[args.workload]
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps * per_step)]
     pending = list(reversed(events))

@@ -193,6 +193,28 @@ int pt_adamw_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
                   double beta1, double beta2, double eps, double weight_decay, double step,
                   void* stream);
 
+/* Gradient clipping fused into the step.  The train loop clips right before the step
+ * (src/picotron/training/train_loop.py:163-168 -> _clip_gradients :338-350 ->
+ * torch.nn.utils.clip_grad_norm_(params, max_norm)), a read of every gradient for the norm
+ * and a read-modify-write to scale them.  Here:
+ *   pt_clip_grad_norm: total_norm = ||all gradients||_2 (fp32 per-block sums of squares,
+ *     added in double in a fixed order) and clip_coef = min(max_norm / (total_norm + 1e-6), 1)
+ *     as torch computes it, written as fp32 scalars to device memory.  `table` has the
+ *     pt_adamw_step layout; only the grad address, numel and first block index are read.
+ *     Workspace: pt_clip_grad_norm_workspace_bytes(total_blocks).  With no records,
+ *     total_norm = 0 and clip_coef = 1.
+ *   pt_adamw_step_scaled: pt_adamw_step with every gradient multiplied by *grad_scale
+ *     (device fp32, e.g. clip_coef) as it is read, g = g * scale as torch's clipping
+ *     leaves it; with write_grad != 0 the scaled gradient is also stored back, so the
+ *     gradients end exactly as after torch's clip_grad_norm_. */
+size_t pt_clip_grad_norm_workspace_bytes(int64_t total_blocks);
+int pt_clip_grad_norm(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                      double max_norm, float* total_norm_out, float* clip_coef_out,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_blocks, double lr,
+                         double beta1, double beta2, double eps, double weight_decay, double step,
+                         const float* grad_scale, int write_grad, void* stream);
+
 /* ---------------------------------------------------------------- Utility
  * Device-to-device copy of `bytes` (multiple of 16, 16-byte aligned pointers) with the
  * same 128-bit load/store pattern as the streaming kernels.  No reference counterpart:

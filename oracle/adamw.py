@@ -44,3 +44,17 @@ def fallback_step(optimizer: torch.optim.Optimizer) -> None:
     """The reference's fallback as it runs: torch's own AdamW step."""
 
     optimizer.step()
+
+
+def clip_grad_norm(grads: list[Tensor], max_norm: float, compute: torch.dtype = torch.float64) -> tuple[Tensor, list[Tensor]]:
+    """torch.nn.utils.clip_grad_norm_ with norm_type 2, as the train loop calls it before
+    the step (reference src/picotron/training/train_loop.py:338-350): total = ||all grads||_2,
+    coef = min(max_norm / (total + 1e-6), 1), every gradient multiplied by coef.  Returns
+    (total, clipped grads) in ``compute``."""
+
+    gs = [g.to(compute) for g in grads]
+    if not gs:
+        return torch.zeros((), dtype=compute), []
+    total = torch.sqrt(sum((g * g).sum() for g in gs))
+    coef = torch.clamp(max_norm / (total + 1e-6), max=1.0)
+    return total, [g * coef for g in gs]

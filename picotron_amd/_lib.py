@@ -83,6 +83,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int64, c_double, c_double, c_double, c_double, c_double, c_double,
          c_void_p],
     ),
+    "pt_clip_grad_norm_workspace_bytes": (c_size_t, [c_int64]),
+    "pt_clip_grad_norm": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_double, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "pt_adamw_step_scaled": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_double, c_double, c_double, c_double, c_double, c_double,
+         c_void_p, c_int, c_void_p],
+    ),
     "pt_copy": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
 }
 

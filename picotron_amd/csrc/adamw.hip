@@ -15,6 +15,15 @@
 // One launch covers every tensor: block b finds its tensor by binary search over the
 // per-tensor first-block indices in the device table, then streams its chunk of
 // kBlockElems elements (16-byte vectors when all four pointers are aligned).
+//
+// Gradient clipping fused into the step (torch.nn.utils.clip_grad_norm_, which the train
+// loop runs right before the step, src/picotron/training/train_loop.py:163-168,338-350):
+// pt_clip_grad_norm computes total_norm = ||all grads||_2 and
+// clip_coef = min(max_norm / (total_norm + 1e-6), 1) on the device (one read of the
+// grads, per-block fp32 partial sums of squares added in double in a fixed order), and
+// pt_adamw_step_scaled multiplies each gradient by that device scalar as it reads it --
+// optionally writing the clipped gradient back -- instead of a separate read-modify-write
+// pass over every gradient.
 #include <cmath>
 
 #include "pt_common.hpp"
@@ -40,6 +49,20 @@ struct AdamScalars {
   float eps;
 };
 
+__device__ __forceinline__ int64_t find_tensor(const AdamRec* __restrict__ table, int64_t ntensors,
+                                               int64_t blk) {
+  int64_t lo = 0, hi = ntensors - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (table[mid].first_block <= blk) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  return lo;
+}
+
 __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
                                           const AdamScalars& s) {
   p = p * s.decay;
@@ -50,23 +73,21 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
   p = p + s.neg_step * __fdiv_rn(m, denom);
 }
 
+// SCALED: the gradient is multiplied by *grad_scale as it is read (torch's clipping
+// multiplies the stored gradient, g = g * coef, before the step reads it), and written back
+// when write_grad != 0.
+template <bool SCALED>
 __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restrict__ table,
-                                                         int64_t ntensors, AdamScalars s) {
+                                                         int64_t ntensors, AdamScalars s,
+                                                         const float* __restrict__ grad_scale,
+                                                         int write_grad) {
   const int64_t blk = blockIdx.x;
-  int64_t lo = 0, hi = ntensors - 1;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi + 1) / 2;
-    if (table[mid].first_block <= blk) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
-    }
-  }
-  const AdamRec r = table[lo];
+  const AdamRec r = table[find_tensor(table, ntensors, blk)];
+  const float gs = SCALED ? *grad_scale : 1.0f;
   const int64_t start = (blk - r.first_block) * kBlockElems;
   const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
   float* P = reinterpret_cast<float*>(r.p);
-  const float* G = reinterpret_cast<const float*>(r.g);
+  float* G = reinterpret_cast<float*>(r.g);
   float* M = reinterpret_cast<float*>(r.m);
   float* Vv = reinterpret_cast<float*>(r.v);
   const bool vec_ok = ((r.p | r.g | r.m | r.v) & 15) == 0;
@@ -87,6 +108,7 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float pp = pv[k][j], mm = mv[k][j], v2 = vv[k][j];
+        if constexpr (SCALED) gv[k][j] = gv[k][j] * gs;
         adam_elem(pp, gv[k][j], mm, v2, s);
         pv[k][j] = pp;
         mv[k][j] = mm;
@@ -95,16 +117,113 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
       __builtin_nontemporal_store(pv[k], reinterpret_cast<f32x4*>(P + i));
       __builtin_nontemporal_store(mv[k], reinterpret_cast<f32x4*>(M + i));
       __builtin_nontemporal_store(vv[k], reinterpret_cast<f32x4*>(Vv + i));
+      if (SCALED && write_grad) __builtin_nontemporal_store(gv[k], reinterpret_cast<f32x4*>(G + i));
     }
   } else {
     for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
       float pp = P[i], mm = M[i], v2 = Vv[i];
-      adam_elem(pp, G[i], mm, v2, s);
+      float g = G[i];
+      if constexpr (SCALED) g = g * gs;
+      adam_elem(pp, g, mm, v2, s);
       P[i] = pp;
       M[i] = mm;
       Vv[i] = v2;
+      if (SCALED && write_grad) G[i] = g;
     }
   }
+}
+
+// Per-block partial sum of squares of the gradients (table layout as the step; only the
+// g, n and first_block fields are read).
+__global__ __launch_bounds__(kThreads) void grad_sumsq_kernel(const AdamRec* __restrict__ table,
+                                                              int64_t ntensors,
+                                                              float* __restrict__ partial) {
+  __shared__ float red[kThreads / 64];
+  const int64_t blk = blockIdx.x;
+  const AdamRec r = table[find_tensor(table, ntensors, blk)];
+  const int64_t start = (blk - r.first_block) * kBlockElems;
+  const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
+  const float* G = reinterpret_cast<const float*>(r.g);
+  float acc = 0.0f;
+  if ((r.g & 15) == 0 && end - start == kBlockElems) {
+    f32x4 gv[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k)
+      gv[k] = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc += gv[k][j] * gv[k][j];
+  } else {
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) acc += G[i] * G[i];
+  }
+  acc = wave_sum(acc);
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+    partial[blk] = t;
+  }
+}
+
+// total_norm = sqrt(sum of the partials, added in double in a fixed order) and torch's
+// clip coefficient, both as fp32 device scalars:
+//   clip_coef = (1 / (total_norm + 1e-6)) * max_norm   (Python's max_norm / tensor)
+//   clip_coef_clamped = clamp(clip_coef, max=1)          (NaN stays NaN)
+__global__ __launch_bounds__(1024) void grad_norm_finish_kernel(const float* __restrict__ partial,
+                                                                int64_t nblocks, float max_norm,
+                                                                float* __restrict__ total_out,
+                                                                float* __restrict__ coef_out) {
+  __shared__ double red[16];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < nblocks; i += 1024) acc += static_cast<double>(partial[i]);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
+  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) t += red[w];
+    const float total = static_cast<float>(sqrt(t));
+    const float denom = total + 1e-6f;
+    const float coef = (1.0f / denom) * max_norm;
+    *total_out = total;
+    *coef_out = coef > 1.0f ? 1.0f : coef;
+  }
+}
+
+AdamScalars host_scalars(double lr, double beta1, double beta2, double eps, double weight_decay,
+                         double step) {
+  // torch.optim.adamw._single_tensor_adamw, in Python floats (double):
+  const double bias_correction1 = 1.0 - std::pow(beta1, step);
+  const double bias_correction2 = 1.0 - std::pow(beta2, step);
+  const double step_size = lr / bias_correction1;
+  const double bc2_sqrt = std::pow(bias_correction2, 0.5);
+  AdamScalars s;
+  s.decay = static_cast<float>(1.0 - lr * weight_decay);
+  s.w1 = static_cast<float>(1.0 - beta1);
+  s.beta2 = static_cast<float>(beta2);
+  s.omb2 = static_cast<float>(1.0 - beta2);
+  s.neg_step = static_cast<float>(-step_size);
+  s.bc2_sqrt = static_cast<float>(bc2_sqrt);
+  s.eps = static_cast<float>(eps);
+  return s;
+}
+
+int check_table(const char* fn, const int64_t* table, int64_t n_tensors, int64_t total_blocks) {
+  const std::string name(fn);
+  if (n_tensors < 0 || total_blocks < 0) return fail(PT_EINVAL, name + ": negative count");
+  if (n_tensors == 0 || total_blocks == 0) return -1;  // nothing to do
+  if (!table) return fail(PT_EINVAL, name + ": null table");
+  if ((reinterpret_cast<uintptr_t>(table) & 7u) != 0)
+    return fail(PT_EINVAL, name + ": table not 8-byte aligned");
+  if (total_blocks * kThreads > 0xffffffffLL)
+    return fail(PT_EUNSUPPORTED, name + ": more than 2^24 blocks in one launch");
+  return PT_OK;
 }
 
 }  // namespace
@@ -119,30 +238,59 @@ int64_t pt_adamw_block_elems(void) { return kBlockElems; }
 int pt_adamw_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks, double lr,
                   double beta1, double beta2, double eps, double weight_decay, double step,
                   void* stream) {
-  if (n_tensors < 0 || total_blocks < 0) return fail(PT_EINVAL, "pt_adamw_step: negative count");
-  if (n_tensors == 0 || total_blocks == 0) return ok();
-  if (!table) return fail(PT_EINVAL, "pt_adamw_step: null table");
-  if ((reinterpret_cast<uintptr_t>(table) & 7u) != 0)
-    return fail(PT_EINVAL, "pt_adamw_step: table not 8-byte aligned");
-  if (total_blocks * kThreads > 0xffffffffLL)
-    return fail(PT_EUNSUPPORTED, "pt_adamw_step: more than 2^24 blocks in one launch");
+  const int rc = check_table("pt_adamw_step", table, n_tensors, total_blocks);
+  if (rc == -1) return ok();
+  if (rc != PT_OK) return rc;
   if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step: step must be >= 1");
-  // torch.optim.adamw._single_tensor_adamw, in Python floats (double):
-  const double bias_correction1 = 1.0 - std::pow(beta1, step);
-  const double bias_correction2 = 1.0 - std::pow(beta2, step);
-  const double step_size = lr / bias_correction1;
-  const double bc2_sqrt = std::pow(bias_correction2, 0.5);
-  AdamScalars s;
-  s.decay = static_cast<float>(1.0 - lr * weight_decay);
-  s.w1 = static_cast<float>(1.0 - beta1);
-  s.beta2 = static_cast<float>(beta2);
-  s.omb2 = static_cast<float>(1.0 - beta2);
-  s.neg_step = static_cast<float>(-step_size);
-  s.bc2_sqrt = static_cast<float>(bc2_sqrt);
-  s.eps = static_cast<float>(eps);
-  hipLaunchKernelGGL(adamw_kernel, dim3(static_cast<unsigned>(total_blocks)), dim3(kThreads), 0,
-                     as_stream(stream), reinterpret_cast<const AdamRec*>(table), n_tensors, s);
+  hipLaunchKernelGGL(adamw_kernel<false>, dim3(static_cast<unsigned>(total_blocks)),
+                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
+                     n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step),
+                     static_cast<const float*>(nullptr), 0);
   return check_launch("pt_adamw_step");
+}
+
+int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_blocks, double lr,
+                         double beta1, double beta2, double eps, double weight_decay, double step,
+                         const float* grad_scale, int write_grad, void* stream) {
+  const int rc = check_table("pt_adamw_step_scaled", table, n_tensors, total_blocks);
+  if (rc == -1) return ok();
+  if (rc != PT_OK) return rc;
+  if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step_scaled: step must be >= 1");
+  if (!grad_scale) return fail(PT_EINVAL, "pt_adamw_step_scaled: null grad_scale");
+  hipLaunchKernelGGL(adamw_kernel<true>, dim3(static_cast<unsigned>(total_blocks)),
+                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
+                     n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step), grad_scale,
+                     write_grad);
+  return check_launch("pt_adamw_step_scaled");
+}
+
+size_t pt_clip_grad_norm_workspace_bytes(int64_t total_blocks) {
+  return total_blocks < 0 ? 0 : static_cast<size_t>(total_blocks) * sizeof(float);
+}
+
+int pt_clip_grad_norm(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                      double max_norm, float* total_norm_out, float* clip_coef_out,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!total_norm_out || !clip_coef_out)
+    return fail(PT_EINVAL, "pt_clip_grad_norm: null output");
+  hipStream_t st = as_stream(stream);
+  int rc = check_table("pt_clip_grad_norm", table, n_tensors, total_blocks);
+  if (rc != -1 && rc != PT_OK) return rc;
+  if (rc == PT_OK) {
+    if (!workspace || workspace_bytes < pt_clip_grad_norm_workspace_bytes(total_blocks) ||
+        !aligned16(workspace))
+      return fail(PT_EINVAL, "pt_clip_grad_norm: workspace too small or not 16-byte aligned");
+    hipLaunchKernelGGL(grad_sumsq_kernel, dim3(static_cast<unsigned>(total_blocks)),
+                       dim3(kThreads), 0, st, reinterpret_cast<const AdamRec*>(table), n_tensors,
+                       static_cast<float*>(workspace));
+    if (int lrc = check_launch("pt_clip_grad_norm")) return lrc;
+  } else {
+    total_blocks = 0;  // no gradients: the norm of nothing is 0
+  }
+  hipLaunchKernelGGL(grad_norm_finish_kernel, dim3(1), dim3(1024), 0, st,
+                     static_cast<const float*>(workspace), total_blocks,
+                     static_cast<float>(max_norm), total_norm_out, clip_coef_out);
+  return check_launch("pt_clip_grad_norm");
 }
 
 }  // extern "C"

@@ -9,6 +9,7 @@ from picotron_amd.nn.triton_kernels.adamw import (
     AdamWStepWithFallback,
     TritonAdamWUnavailable,
     triton_adamw_step,
+    triton_clip_grad_norm_and_step,
 )
 from picotron_amd.nn.triton_kernels.attention import (
     TritonAttentionUnavailable,
@@ -54,4 +55,5 @@ __all__ = [
     # additions beyond the reference surface
     "triton_adamw_step",
     "triton_apply_rotary_embedding_pair",
+    "triton_clip_grad_norm_and_step",
 ]

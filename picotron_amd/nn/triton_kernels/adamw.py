@@ -14,6 +14,12 @@ Supported: fp32 dense parameters and gradients on a gfx950 device, ``amsgrad=Fal
 ``maximize=False``, ``capturable=False``, ``differentiable=False``, float ``lr``.  Anything
 else raises :class:`TritonAdamWUnavailable` (a ``RuntimeError`` whose message says "not
 implemented"), and the fallback runs torch's own step.
+
+``triton_clip_grad_norm_and_step(optimizer, max_norm)`` fuses the gradient clipping the
+train loop runs right before the step (reference src/picotron/training/train_loop.py:163-168
+and ``_clip_gradients`` :338-350, i.e. ``torch.nn.utils.clip_grad_norm_``): one kernel reads
+the gradients for the norm and the clip coefficient stays on the device, where the step
+applies it as it reads each gradient, instead of a separate read-modify-write pass.
 """
 
 from __future__ import annotations
@@ -62,20 +68,25 @@ def _check_param(p: Tensor) -> None:
 
 
 _table_cache: dict[tuple, Tensor] = {}
+_TABLE_CACHE_SIZE = 16
 
 
-def _device_table(key: tuple, host_table: Tensor, device: torch.device) -> Tensor:
-    cached = _table_cache.get(key)
-    if cached is not None:
-        return cached
-    _table_cache.clear()
-    table = host_table.pin_memory().to(device, non_blocking=True)
-    _table_cache[key] = table
-    return table
+def _device_table(host_table: Tensor, device: torch.device) -> Tensor:
+    """The device copy of a record table, cached by content (tables repeat every step)."""
+
+    key = (device, tuple(host_table.flatten().tolist()))
+    cached = _table_cache.pop(key, None)
+    if cached is None:
+        cached = host_table.pin_memory().to(device, non_blocking=True)
+    _table_cache[key] = cached  # most recent last
+    while len(_table_cache) > _TABLE_CACHE_SIZE:
+        del _table_cache[next(iter(_table_cache))]
+    return cached
 
 
-def triton_adamw_step(optimizer: Optimizer) -> None:
-    """One AdamW step of ``optimizer`` with the fused HIP kernel (or raise unavailable)."""
+def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.device | None]:
+    """Validate everything the fused step needs, touching no state; returns the parameter
+    groups with their parameters that have gradients, and the device."""
 
     if not isinstance(optimizer, torch.optim.AdamW):
         raise _reject(f"{type(optimizer).__name__} (only torch.optim.AdamW)")
@@ -92,7 +103,7 @@ def triton_adamw_step(optimizer: Optimizer) -> None:
                 raise _reject("parameters on several devices")
         groups.append((group, params))
     if device is None:
-        return
+        return groups, None
     reason = _lib.unavailable_reason()
     if reason is not None:
         raise TritonAdamWUnavailable(f"HIP kernel library unavailable: {reason}")
@@ -101,11 +112,19 @@ def triton_adamw_step(optimizer: Optimizer) -> None:
     # Every check that can fail happens before any optimizer state is touched, so a
     # fallback to optimizer.step() never sees a half-applied step.
     per_block = ops.adamw_block_elems()
+    total = 0
     for _, params in groups:
         blocks = sum((p.numel() + per_block - 1) // per_block for p in params)
+        total += blocks
         if blocks * 256 > 0xFFFFFFFF:
             raise _reject("parameter groups above 2^24 blocks of elements")
+    if total * 256 > 0xFFFFFFFF:
+        raise _reject("more than 2^24 blocks of gradient elements")
+    return groups, device
 
+
+def _run(optimizer: Optimizer, groups, device: torch.device, grad_scale: Tensor | None,
+         write_grad: bool) -> None:
     for group, params in groups:
         if not params:
             continue
@@ -128,12 +147,43 @@ def triton_adamw_step(optimizer: Optimizer) -> None:
             host_table, total_blocks = ops.adamw_table(ps, grads, exp_avgs, exp_avg_sqs)
             if total_blocks == 0:
                 continue
-            key = tuple(host_table.flatten().tolist())
-            table = _device_table(key, host_table, device)
-            ops.adamw_step(
-                table, total_blocks, lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
-                weight_decay=group["weight_decay"], step=step,
-            )
+            table = _device_table(host_table, device)
+            hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
+                         weight_decay=group["weight_decay"], step=step)
+            if grad_scale is None:
+                ops.adamw_step(table, total_blocks, **hyper)
+            else:
+                ops.adamw_step_scaled(table, total_blocks, grad_scale, write_grad=write_grad, **hyper)
+
+
+def triton_adamw_step(optimizer: Optimizer) -> None:
+    """One AdamW step of ``optimizer`` with the fused HIP kernel (or raise unavailable)."""
+
+    groups, device = _plan(optimizer)
+    if device is not None:
+        _run(optimizer, groups, device, None, False)
+
+
+def triton_clip_grad_norm_and_step(
+    optimizer: Optimizer, max_norm: float, *, write_back_grads: bool = True
+) -> Tensor:
+    """``torch.nn.utils.clip_grad_norm_(params, max_norm)`` followed by ``optimizer.step()``
+    for a ``torch.optim.AdamW``, fused: returns the total gradient norm (fp32 scalar tensor).
+
+    The norm covers every parameter of the optimizer that has a gradient (the train loop's
+    model.parameters()).  With ``write_back_grads`` the gradients are left clipped, exactly
+    as ``clip_grad_norm_`` leaves them; without it they keep their unclipped values (one
+    write of every gradient less) while the update still uses the clipped ones.
+    """
+
+    groups, device = _plan(optimizer)
+    if device is None:
+        return torch.tensor(0.0)
+    grads = [p.grad for _, params in groups for p in params]
+    host_table, total_blocks = ops.adamw_table(grads, grads, grads, grads)
+    total_norm, coef = ops.clip_grad_norm(_device_table(host_table, device), total_blocks, float(max_norm))
+    _run(optimizer, groups, device, coef, write_back_grads)
+    return total_norm
 
 
 class AdamWStepWithFallback:
@@ -144,10 +194,16 @@ class AdamWStepWithFallback:
         self.use_triton = use_triton
         self._fallback_warned = False
 
-    def step(self, optimizer: Optimizer) -> None:
+    def step(self, optimizer: Optimizer, max_grad_norm: float | None = None) -> None:
+        """``optimizer.step()``; with ``max_grad_norm`` the gradients are first clipped as
+        ``torch.nn.utils.clip_grad_norm_`` does (fused into the step on the fast path)."""
+
         if self.use_triton:
             try:
-                triton_adamw_step(optimizer)
+                if max_grad_norm is None:
+                    triton_adamw_step(optimizer)
+                else:
+                    triton_clip_grad_norm_and_step(optimizer, max_grad_norm)
                 return
             except Exception as error:
                 if not self._fallback_warned:
@@ -157,4 +213,7 @@ class AdamWStepWithFallback:
                         stacklevel=2,
                     )
                     self._fallback_warned = True
+        if max_grad_norm is not None:
+            params = [p for group in optimizer.param_groups for p in group["params"]]
+            torch.nn.utils.clip_grad_norm_(params, max_grad_norm)
         optimizer.step()

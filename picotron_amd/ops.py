@@ -405,6 +405,49 @@ def adamw_step(
     )
 
 
+def adamw_step_scaled(
+    table_device: Tensor,
+    total_blocks: int,
+    grad_scale: Tensor,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: float,
+    write_grad: bool,
+) -> None:
+    """:func:`adamw_step` with every gradient multiplied by the fp32 device scalar
+    ``grad_scale`` as it is read (and stored back when ``write_grad``)."""
+
+    device = _check_cuda(table_device, grad_scale)
+    if grad_scale.dtype != torch.float32 or grad_scale.numel() != 1:
+        raise ValueError("grad_scale must be one fp32 element")
+    _lib.call(
+        "pt_adamw_step_scaled",
+        table_device.data_ptr(), table_device.size(0), int(total_blocks), float(lr), float(beta1),
+        float(beta2), float(eps), float(weight_decay), float(step), grad_scale.data_ptr(),
+        int(write_grad), _stream(device),
+    )
+
+
+def clip_grad_norm(table_device: Tensor, total_blocks: int, max_norm: float) -> tuple[Tensor, Tensor]:
+    """(total_norm, clip_coef) fp32 device scalars over the gradients of a table built by
+    :func:`adamw_table`: torch.nn.utils.clip_grad_norm_'s norm and clamped coefficient."""
+
+    device = _check_cuda(table_device)
+    out = torch.empty(2, dtype=torch.float32, device=device)
+    ws_bytes = _lib.lib().pt_clip_grad_norm_workspace_bytes(int(total_blocks))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
+    _lib.call(
+        "pt_clip_grad_norm",
+        table_device.data_ptr(), table_device.size(0), int(total_blocks), float(max_norm),
+        out.data_ptr(), out.data_ptr() + 4, ws.data_ptr(), ws_bytes, _stream(device),
+    )
+    return out[0], out[1:2]
+
+
 # ------------------------------------------------------------------ utility
 
 

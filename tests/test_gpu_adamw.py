@@ -106,3 +106,94 @@ def test_full_config(gpu):
         close_fp32(p.detach()[lo:hi], ep)
         close_fp32(opt.state[p]["exp_avg"][lo:hi], em)
         close_fp32(opt.state[p]["exp_avg_sq"][lo:hi], ev)
+
+
+def _clip_pair(gpu, sizes, seed):
+    fused = [torch.nn.Parameter(randn((n,), torch.float32, gpu, seed + n, 0.02)) for n in sizes]
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in fused]
+    return fused, ref
+
+
+@pytest.mark.parametrize("max_norm", [0.05, 1e4])
+def test_clip_grad_norm_and_step_matches_torch(gpu, max_norm):
+    # torch.nn.utils.clip_grad_norm_ then torch AdamW (the reference train loop) against the
+    # fused clip + step: clipping active (norm ~ 1.3) and inactive (coefficient exactly 1)
+    from picotron_amd.nn.triton_kernels import triton_clip_grad_norm_and_step
+
+    sizes = [1, 3, 4095, 4096, 4097, 70_000, 1 << 20]
+    fused, ref = _clip_pair(gpu, sizes, 7)
+    opt_f = torch.optim.AdamW(fused, **HP)
+    opt_r = torch.optim.AdamW(ref, foreach=False, **HP)
+    for step in range(3):
+        for i, (a, b) in enumerate(zip(fused, ref)):
+            g = randn(a.shape, torch.float32, gpu, 50 * step + i, 1e-3)
+            a.grad, b.grad = g, g.clone()
+        ref_total = torch.nn.utils.clip_grad_norm_(ref, max_norm)
+        opt_r.step()
+        total = triton_clip_grad_norm_and_step(opt_f, max_norm)
+        close_fp32(total.reshape(()), ref_total.reshape(()))
+        for a, b in zip(fused, ref):
+            close_fp32(a.grad, b.grad)  # left clipped, as clip_grad_norm_ leaves them
+            if max_norm > 1e3:
+                assert torch.equal(a.grad, b.grad)
+    for a, b in zip(fused, ref):
+        close_fp32(a.detach(), b.detach())
+        close_fp32(opt_f.state[a]["exp_avg"], opt_r.state[b]["exp_avg"])
+        close_fp32(opt_f.state[a]["exp_avg_sq"], opt_r.state[b]["exp_avg_sq"])
+
+
+def test_clip_without_write_back_and_the_oracle(gpu):
+    from picotron_amd.nn.triton_kernels import triton_clip_grad_norm_and_step
+
+    sizes = [5000, 123, 4096 * 3]
+    fused, _ = _clip_pair(gpu, sizes, 9)
+    grads = [randn(p.shape, torch.float32, gpu, 900 + i, 0.05) for i, p in enumerate(fused)]
+    for p, g in zip(fused, grads):
+        p.grad = g.clone()
+    p0 = [p.detach().clone() for p in fused]
+    opt = torch.optim.AdamW(fused, **HP)
+    total = triton_clip_grad_norm_and_step(opt, 0.5, write_back_grads=False)
+    ref_total, clipped = o_adamw.clip_grad_norm(grads, 0.5)
+    assert abs(total.item() - ref_total.item()) <= 1e-6 * ref_total.item()
+    for p, g, c, q in zip(fused, grads, clipped, p0):
+        assert torch.equal(p.grad, g)  # gradients keep their unclipped values
+        ep, _, _ = o_adamw.step(q, c, torch.zeros_like(q), torch.zeros_like(q), t=1, lr=HP["lr"],
+                                beta1=HP["betas"][0], beta2=HP["betas"][1], eps=HP["eps"],
+                                weight_decay=HP["weight_decay"])
+        close_fp32(p.detach(), ep.float())
+
+
+def test_clip_non_finite_gradients_propagate_like_torch(gpu):
+    from picotron_amd.nn.triton_kernels import triton_clip_grad_norm_and_step
+
+    fused, ref = _clip_pair(gpu, [4096, 10], 11)
+    for a, b in zip(fused, ref):
+        g = randn(a.shape, torch.float32, gpu, 3, 1e-3)
+        a.grad, b.grad = g, g.clone()
+    fused[1].grad[3] = float("inf")
+    ref[1].grad[3] = float("inf")
+    ref_total = torch.nn.utils.clip_grad_norm_(ref, 1.0)
+    torch.optim.AdamW(ref, foreach=False, **HP).step()
+    total = triton_clip_grad_norm_and_step(torch.optim.AdamW(fused, **HP), 1.0)
+    assert torch.isinf(total) and torch.isinf(ref_total)
+    for a, b in zip(fused, ref):
+        assert torch.equal(torch.isnan(a.detach()), torch.isnan(b.detach()))
+        assert torch.equal(torch.isnan(a.grad), torch.isnan(b.grad))
+
+
+def test_stepper_with_clipping_and_no_gradients(gpu):
+    from picotron_amd.nn.triton_kernels import triton_clip_grad_norm_and_step
+
+    p = torch.nn.Parameter(torch.ones(8, device=gpu))
+    opt = torch.optim.AdamW([p], **HP)
+    assert float(triton_clip_grad_norm_and_step(opt, 1.0)) == 0.0  # nothing has a gradient
+    assert len(opt.state) == 0
+    fused, ref = _clip_pair(gpu, [300], 13)
+    fused[0].grad = torch.full_like(fused[0], 2.0)
+    ref[0].grad = torch.full_like(ref[0], 2.0)
+    stepper = AdamWStepWithFallback(use_triton=True)
+    stepper.step(torch.optim.AdamW(fused, **HP), max_grad_norm=1.0)
+    assert not stepper._fallback_warned
+    torch.nn.utils.clip_grad_norm_(ref, 1.0)
+    torch.optim.AdamW(ref, foreach=False, **HP).step()
+    close_fp32(fused[0].detach(), ref[0].detach())

@@ -316,3 +316,20 @@ def test_cross_entropy_shifted_oracle_matches_torch_autograd_through_the_slice()
     torch.testing.assert_close(loss, ref.detach(), rtol=1e-12, atol=1e-12)
     torch.testing.assert_close(grad, lr.grad, rtol=1e-10, atol=1e-12)
     assert torch.equal(grad[:, -1, :], torch.zeros(b, v, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("max_norm", [0.5, 1e6])
+def test_clip_grad_norm_oracle_matches_torch_library(max_norm):
+    torch.manual_seed(11)
+    grads = [torch.randn(n, dtype=torch.float64) * s for n, s in ((7, 1.0), (300, 0.1), (1, 3.0))]
+    params = [torch.nn.Parameter(torch.zeros_like(g)) for g in grads]
+    for p, g in zip(params, grads):
+        p.grad = g.clone()
+    ref_total = torch.nn.utils.clip_grad_norm_(params, max_norm)
+    total, clipped = o_adamw.clip_grad_norm(grads, max_norm)
+    torch.testing.assert_close(total, ref_total, rtol=1e-12, atol=0)
+    for c, p in zip(clipped, params):
+        torch.testing.assert_close(c, p.grad, rtol=1e-12, atol=0)
+    if max_norm > 1e3:  # below the norm: the coefficient clamps to exactly 1
+        for c, g in zip(clipped, grads):
+            assert torch.equal(c, g)

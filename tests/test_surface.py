@@ -174,6 +174,24 @@ def test_shifted_cross_entropy_cpu_fallback_is_the_train_loop_expression():
     torch.testing.assert_close(plain(logits, ids, shift=True), actual)
 
 
+def test_adamw_clip_fallback_is_clip_grad_norm_then_step():
+    torch.manual_seed(4)
+    ref_params = [torch.nn.Parameter(torch.randn(5)), torch.nn.Parameter(torch.randn(3, 2))]
+    params = [torch.nn.Parameter(p.detach().clone()) for p in ref_params]
+    for p, q in zip(ref_params, params):
+        p.grad = torch.randn_like(p) * 4
+        q.grad = p.grad.clone()
+    ref_opt = AdamW(ref_params, lr=0.01, weight_decay=0.1)
+    torch.nn.utils.clip_grad_norm_(ref_params, 1.0)
+    ref_opt.step()
+    stepper = AdamWStepWithFallback(use_triton=True)
+    with pytest.warns(RuntimeWarning, match="Triton AdamW unavailable"):
+        stepper.step(AdamW(params, lr=0.01, weight_decay=0.1), max_grad_norm=1.0)
+    for p, q in zip(ref_params, params):
+        torch.testing.assert_close(q, p, rtol=0, atol=0)
+        torch.testing.assert_close(q.grad, p.grad, rtol=0, atol=0)
+
+
 def test_adamw_fallback_matches_known_single_step_update():
     parameter = torch.nn.Parameter(torch.tensor([1.0]))
     optimizer = AdamW([parameter], lr=0.1, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
