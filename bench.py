@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|copy]
 
 Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
 (8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
@@ -184,6 +184,125 @@ class RMSNormWorkload(Workload):
             sample=f"one activation [{rows}, {c}] (one of the step's {self.layers} layers): reference PyTorch "
                    f"fallback fwd+bwd (rmsnorm.py:56-60,113-134) on bf16 CPU tensors, median of {calls} calls "
                    f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=rows / sec,
+        )
+
+
+class ResidualRMSNormWorkload(Workload):
+    """The decoder block's residual add fused with the norm after it (reference
+    src/picotron/models/picotron_decoder.py:116-119), forward and backward."""
+
+    name = "residual_rmsnorm"
+    metric = "Residual add + RMSNorm fwd+bwd HBM GB/s & % of peak, 16k tok x 4096 bf16"
+    rows, cols, eps = 16384, 4096, 1e-5
+
+    def __init__(self, layers: int) -> None:
+        self.layers = layers
+        r, c = self.rows, self.cols
+        bf = torch.bfloat16
+        self.w = _seeded((c,), bf, 2, 0.02, 1.0)
+        self.x = [_seeded((r, c), bf, 30 + i) for i in range(layers)]
+        self.res = [_seeded((r, c), bf, 40 + i) for i in range(layers)]
+        self.dy = [_seeded((r, c), bf, 50 + i) for i in range(layers)]
+        self.dh_in = [_seeded((r, c), bf, 60 + i) for i in range(layers)]
+        self.h = [torch.empty_like(t) for t in self.x]
+        self.y = [torch.empty_like(t) for t in self.x]
+        self.dh = [torch.empty_like(t) for t in self.x]
+        self.rstd = [torch.empty(r, dtype=torch.float32, device="cuda") for _ in range(layers)]
+        self.dw = [torch.empty(c, dtype=bf, device="cuda") for _ in range(layers)]
+        lib = _lib.lib()
+        self.lib = lib
+        self.ws_bytes = lib.pt_rmsnorm_bwd_workspace_bytes(r, c, _lib.PT_BFLOAT16)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
+        s = 2
+        self.fwd_bytes = 4 * r * c * s + c * s + 4 * r
+        self.bwd_bytes = 4 * r * c * s + 2 * c * s + 4 * r
+        self.bytes_per_step = layers * (self.fwd_bytes + self.bwd_bytes)
+        self.tokens_per_step = layers * r
+        self.dominant = "fused residual + rmsnorm backward (rmsnorm_bwd_kernel with dh_in + rmsnorm_dw_finish_kernel)"
+        self.dominant_bytes = self.bwd_bytes
+        self.description = (
+            f"h = x + residual; y = RMSNorm(h) and its backward dh = norm_bwd(dy) + dh_in, bf16 "
+            f"[16384 tokens, 4096], eps 1e-5, bf16 weight; step = forward of {layers} layers then "
+            f"backward in reverse"
+        )
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        bfc = _lib.PT_BFLOAT16
+        self._fwd = [
+            (lib.pt_residual_rmsnorm_fwd, (_p(self.x[i]), c, _p(self.res[i]), c, _p(self.w), _p(self.h[i]), c,
+                                           _p(self.y[i]), c, _p(self.rstd[i]), r, c, ctypes.c_float(self.eps),
+                                           bfc, bfc, self.stream))
+            for i in range(layers)
+        ]
+        self._bwd = [
+            (lib.pt_residual_rmsnorm_bwd, (_p(self.dy[i]), c, _p(self.dh_in[i]), c, _p(self.h[i]), c, _p(self.w),
+                                           _p(self.rstd[i]), _p(self.dh[i]), c, _p(self.dw[i]), _p(self.ws),
+                                           self.ws_bytes, r, c, bfc, bfc, self.stream))
+            for i in range(layers)
+        ]
+
+    def step(self, events):
+        for fn, args in self._fwd:
+            rc = fn(*args)
+            if rc:
+                _lib.check("pt_residual_rmsnorm_fwd", rc)
+        for fn, args in reversed(self._bwd):
+            if events is not None:
+                start, end = events.pop()
+                start.record()
+            rc = fn(*args)
+            if events is not None:
+                end.record()
+            if rc:
+                _lib.check("pt_residual_rmsnorm_bwd", rc)
+
+    def extra(self, steps: int) -> dict:
+        """The same step unfused: torch's add, then the plain norm kernels, then torch's add of
+        the two gradients of h."""
+
+        lib, r, c, bfc = self.lib, self.rows, self.cols, _lib.PT_BFLOAT16
+
+        def unfused():
+            for i in range(self.layers):
+                torch.add(self.x[i], self.res[i], out=self.h[i])
+                _lib.check("pt_rmsnorm_fwd", lib.pt_rmsnorm_fwd(
+                    _p(self.h[i]), c, _p(self.w), _p(self.y[i]), c, _p(self.rstd[i]), r, c,
+                    ctypes.c_float(self.eps), bfc, bfc, self.stream))
+            for i in reversed(range(self.layers)):
+                _lib.check("pt_rmsnorm_bwd", lib.pt_rmsnorm_bwd(
+                    _p(self.dy[i]), c, _p(self.h[i]), c, _p(self.w), _p(self.rstd[i]), _p(self.dh[i]), c,
+                    _p(self.dw[i]), _p(self.ws), self.ws_bytes, r, c, bfc, bfc, self.stream))
+                self.dh[i].add_(self.dh_in[i])
+
+        unfused()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            unfused()
+        torch.cuda.synchronize()
+        return {"unfused_add_then_norm_ms_per_step": round((time.perf_counter() - t0) / steps * 1e3, 4)}
+
+    def cpu_baseline(self) -> dict:
+        from oracle import rmsnorm as o_rms
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        rows = self.rows
+        x, res, w = self.x[0].cpu(), self.res[0].cpu(), self.w.cpu()
+        dy, dh_in = self.dy[0].cpu(), self.dh_in[0].cpu()
+
+        def call():
+            h = x + res
+            o_rms.fallback_forward_backward(h, w, self.eps, dy)[2].add_(dh_in)
+
+        sec, calls = _time_cpu(call)
+        c = self.cols
+        nbytes = 8 * rows * c * 2 + 3 * c * 2 + 8 * rows
+        return dict(
+            value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"one layer [{rows}, {c}]: bf16 add, the reference PyTorch RMSNorm fallback fwd+bwd "
+                   f"(rmsnorm.py:56-60,113-134) and the add of the two gradients of h, on CPU, median "
+                   f"of {calls} calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
 
@@ -647,6 +766,7 @@ class CopyWorkload(Workload):
 
 WORKLOADS = {
     "rmsnorm": RMSNormWorkload,
+    "residual_rmsnorm": ResidualRMSNormWorkload,
     "swiglu": SwiGLUWorkload,
     "rope": RoPEWorkload,
     "ce": CrossEntropyWorkload,
@@ -656,7 +776,7 @@ WORKLOADS = {
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
+DEFAULT_LAYERS = {"rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
                   "copy": 4}
 
 
@@ -713,7 +833,7 @@ def main() -> int:
     # Pass 2 (the roofline): the same K steps again with a HIP event pair around every
     # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
     # records add a few microseconds per launch, so this pass is not used for the value.
-    per_step = {"rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
+    per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
                 "adamw_clip": 1, "copy": layers}[args.workload]
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps * per_step)]

@@ -79,6 +79,30 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
                    void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
                    int64_t cols, int x_dtype, int w_dtype, void* stream);
 
+/* Residual add fused with the norm that follows it in the decoder block
+ * (src/picotron/models/picotron_decoder.py:116-119: hidden = hidden + attention(...), then
+ * mlp_norm(hidden)):  h = x + residual, computed in fp32 and rounded to x's type, is written,
+ * and y = rmsnorm(h) as pt_rmsnorm_fwd computes it from the rounded h (rstd as there).  One
+ * pass instead of an add pass plus a norm pass that re-reads h.  x, residual, h and y share
+ * x_dtype; h must not be x, residual or y. */
+int pt_residual_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* residual,
+                            int64_t residual_row_stride, const void* weight, void* h,
+                            int64_t h_row_stride, void* y, int64_t y_row_stride, float* rstd,
+                            int64_t rows, int64_t cols, float eps, int x_dtype, int w_dtype,
+                            void* stream);
+
+/* Backward of the fused add + norm.  h also feeds the block's final residual add, so its
+ * gradient is the norm's input gradient plus the gradient arriving from that add:
+ *   dh = rmsnorm_backward(dy; h, weight, rstd) + dh_in   (fp32, rounded once)
+ * which is also the gradient of both x and residual.  dh_in may be NULL (then this is
+ * pt_rmsnorm_bwd with dx = dh) and dh may be the same buffer as dh_in (accumulate in place).
+ * dweight and the workspace as in pt_rmsnorm_bwd. */
+int pt_residual_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* dh_in,
+                            int64_t dh_in_row_stride, const void* h, int64_t h_row_stride,
+                            const void* weight, const float* rstd, void* dh, int64_t dh_row_stride,
+                            void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
+                            int64_t cols, int x_dtype, int w_dtype, void* stream);
+
 /* ---------------------------------------------------------------- SwiGLU
  * out = gate * sigmoid(gate) * up over n contiguous elements (fp32 math).
  * Replaces _swiglu_kernel + _run_triton_forward (src/picotron/nn/triton_kernels/

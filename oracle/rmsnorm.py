@@ -54,3 +54,28 @@ def fallback_forward_backward(
     dx = inverse_rms * (weighted_grad - xf * inverse_rms.square() * dot_mean)
     dw = (g * xf * inverse_rms).reshape(-1, w.numel()).sum(dim=0)
     return y, inverse_rms.squeeze(-1), dx.to(x.dtype), dw.to(w.dtype)
+
+
+def residual_forward(
+    x: Tensor, residual: Tensor, w: Tensor, eps: float, compute: torch.dtype = torch.float64
+) -> tuple[Tensor, Tensor, Tensor]:
+    """The decoder block's residual add and the norm after it (reference
+    src/picotron/models/picotron_decoder.py:116-119): h = x + residual as stored in x's dtype
+    (torch adds in fp32 and rounds once), then (y, rstd) of the norm of that stored h.
+    Returns (h in x's dtype, y in compute, rstd in compute)."""
+
+    h = (x.float() + residual.float()).to(x.dtype) if x.dtype != torch.float64 else x + residual
+    y, rstd = forward(h, w, eps, compute)
+    return h, y, rstd
+
+
+def residual_backward(
+    dy: Tensor, dh_in: Tensor | None, h: Tensor, w: Tensor, eps: float, compute: torch.dtype = torch.float64
+) -> tuple[Tensor, Tensor]:
+    """(dh, dW): dh = the norm's input gradient + dh_in (the gradient reaching h from the
+    block's final residual add); dh is also the gradient of x and of residual."""
+
+    dx, dw = backward(dy, h, w, eps, compute)
+    if dh_in is not None:
+        dx = dx + dh_in.to(compute)
+    return dx, dw

@@ -69,36 +69,44 @@ int validate(const char* fn, int64_t rows, int64_t cols, int xdt, int wdt, bool 
 }  // namespace rmsnorm
 }  // namespace pt
 
-using namespace pt;
-using namespace pt::rmsnorm;
+namespace pt {
+namespace rmsnorm {
+namespace {
 
-extern "C" {
-
-int pt_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* weight, void* y,
-                   int64_t y_row_stride, float* rstd, int64_t rows, int64_t cols, float eps,
-                   int x_dtype, int w_dtype, void* stream) {
+int fwd_impl(const char* fn, const void* x, int64_t xs, const void* res, int64_t res_s,
+             const void* weight, void* h, int64_t hs, void* y, int64_t ys, float* rstd,
+             int64_t rows, int64_t cols, float eps, int x_dtype, int w_dtype, void* stream) {
+  const std::string name(fn);
   Shape s;
-  if (int rc = validate("pt_rmsnorm_fwd", rows, cols, x_dtype, w_dtype, false, &s)) return rc;
+  if (int rc = validate(fn, rows, cols, x_dtype, w_dtype, false, &s)) return rc;
   if (rows == 0) return ok();
-  if (!x || !weight || !y || !rstd) return fail(PT_EINVAL, "pt_rmsnorm_fwd: null pointer");
-  if (rows > 1 && (x_row_stride < cols || y_row_stride < cols))
-    return fail(PT_EINVAL, "pt_rmsnorm_fwd: row stride smaller than cols");
+  const bool fused = res != nullptr || h != nullptr;
+  if (!x || !weight || !y || !rstd || (fused && (!res || !h)))
+    return fail(PT_EINVAL, name + ": null pointer");
+  if (rows > 1 && (xs < cols || ys < cols || (fused && (res_s < cols || hs < cols))))
+    return fail(PT_EINVAL, name + ": row stride smaller than cols");
+  if (fused && (h == x || h == res || h == y))
+    return fail(PT_EINVAL, name + ": h must not alias x, residual or y");
   const int vec = 16 / dtype_size(x_dtype);
   FwdArgs a{};
   a.x = x;
-  a.xs = x_row_stride;
+  a.xs = xs;
   a.w = weight;
   a.wdt = w_dtype;
   a.y = y;
-  a.ys = y_row_stride;
+  a.ys = ys;
   a.rstd = rstd;
   a.rows = rows;
   a.cols = static_cast<int>(cols);
   a.eps = eps;
   a.xdt = x_dtype;
-  a.aligned = (cols % vec == 0) && rows_aligned(x_dtype, x, x_row_stride) &&
-              rows_aligned(x_dtype, y, y_row_stride) && aligned16(weight) &&
-              vector_weight(x_dtype, w_dtype);
+  a.res = fused ? res : nullptr;
+  a.res_s = res_s;
+  a.h = fused ? h : nullptr;
+  a.h_s = hs;
+  a.aligned = (cols % vec == 0) && rows_aligned(x_dtype, x, xs) && rows_aligned(x_dtype, y, ys) &&
+              (!fused || (rows_aligned(x_dtype, res, res_s) && rows_aligned(x_dtype, h, hs))) &&
+              aligned16(weight) && vector_weight(x_dtype, w_dtype);
   a.shape = a.aligned ? s : unaligned_shape(cols, vec);
   a.blocks = fwd_blocks(rows, a.shape, num_cus());
   a.st = as_stream(stream);
@@ -110,8 +118,95 @@ int pt_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* weight, void
   } else {
     launched = launch_fwd<__bf16>(a);
   }
-  if (!launched) return fail(PT_EUNSUPPORTED, "pt_rmsnorm_fwd: no kernel for this shape");
-  return check_launch("pt_rmsnorm_fwd");
+  if (!launched) return fail(PT_EUNSUPPORTED, name + ": no kernel for this shape");
+  return check_launch(fn);
+}
+
+int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int64_t dh_in_s,
+             const void* x, int64_t xs, const void* weight, const float* rstd, void* dx,
+             int64_t dxs, void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
+             int64_t cols, int x_dtype, int w_dtype, void* stream) {
+  const std::string name(fn);
+  Shape s;
+  if (int rc = validate(fn, rows, cols, x_dtype, w_dtype, true, &s)) return rc;
+  hipStream_t st = as_stream(stream);
+  if (rows == 0) {
+    // Empty batch: the weight gradient is a sum over no rows.
+    if (dweight) return fill(dweight, cols, dtype_size(w_dtype), 0u, st);
+    return ok();
+  }
+  if (!dy || !x || !weight || !rstd || (dh_in && !dx))
+    return fail(PT_EINVAL, name + ": null pointer");
+  if (rows > 1 && (dys < cols || xs < cols || (dx && dxs < cols) || (dh_in && dh_in_s < cols)))
+    return fail(PT_EINVAL, name + ": row stride smaller than cols");
+  const int vec = 16 / dtype_size(x_dtype);
+  BwdArgs a{};
+  a.aligned = (cols % vec == 0) && rows_aligned(x_dtype, dy, dys) &&
+              rows_aligned(x_dtype, x, xs) && (dx == nullptr || rows_aligned(x_dtype, dx, dxs)) &&
+              (dh_in == nullptr || rows_aligned(x_dtype, dh_in, dh_in_s)) && aligned16(weight) &&
+              vector_weight(x_dtype, w_dtype);
+  a.shape = a.aligned ? s : unaligned_shape(cols, vec);
+  a.blocks = bwd_blocks(rows, a.shape);
+  float* partial = nullptr;
+  if (dweight) {
+    const size_t need = static_cast<size_t>(a.blocks) * static_cast<size_t>(cols) * sizeof(float);
+    if (!workspace || workspace_bytes < need)
+      return fail(PT_EINVAL, name + ": workspace smaller than pt_rmsnorm_bwd_workspace_bytes()");
+    if (!aligned16(workspace)) return fail(PT_EINVAL, name + ": workspace not aligned");
+    // LDS combining the row slots' weight-gradient sums holds one fp32 per column.
+    if (bwd_waves(a.shape) / a.shape.wpr > 1 && cols * 4 > 160 * 1024)
+      return fail(PT_EUNSUPPORTED, name + ": hidden size too large for the LDS combine");
+    partial = static_cast<float*>(workspace);
+  }
+  a.dy = dy;
+  a.dys = dys;
+  a.x = x;
+  a.xs = xs;
+  a.w = weight;
+  a.wdt = w_dtype;
+  a.rstd = rstd;
+  a.dx = dx;
+  a.dxs = dxs;
+  a.partial = partial;
+  a.rows = rows;
+  a.cols = static_cast<int>(cols);
+  a.xdt = x_dtype;
+  a.st = st;
+  a.dh_in = dh_in;
+  a.dh_in_s = dh_in_s;
+  bool launched;
+  if (x_dtype == PT_FLOAT32) {
+    launched = launch_bwd<float>(a);
+  } else if (x_dtype == PT_FLOAT16) {
+    launched = launch_bwd<_Float16>(a);
+  } else {
+    launched = launch_bwd<__bf16>(a);
+  }
+  if (!launched) return fail(PT_EUNSUPPORTED, name + ": no kernel for this shape");
+  if (int rc = check_launch(fn)) return rc;
+  if (dweight) {
+    const unsigned fblocks = static_cast<unsigned>((cols + kFinishCols - 1) / kFinishCols);
+    hipLaunchKernelGGL(rmsnorm_dw_finish_kernel, dim3(fblocks), dim3(256), 0, st, partial,
+                       a.blocks, static_cast<int>(cols), dweight, w_dtype);
+    return check_launch(fn);
+  }
+  return ok();
+}
+
+}  // namespace
+}  // namespace rmsnorm
+}  // namespace pt
+
+using namespace pt;
+using namespace pt::rmsnorm;
+
+extern "C" {
+
+int pt_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* weight, void* y,
+                   int64_t y_row_stride, float* rstd, int64_t rows, int64_t cols, float eps,
+                   int x_dtype, int w_dtype, void* stream) {
+  return fwd_impl("pt_rmsnorm_fwd", x, x_row_stride, nullptr, 0, weight, nullptr, 0, y,
+                  y_row_stride, rstd, rows, cols, eps, x_dtype, w_dtype, stream);
 }
 
 size_t pt_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols, int x_dtype) {
@@ -130,68 +225,31 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
                    const void* weight, const float* rstd, void* dx, int64_t dx_row_stride,
                    void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
                    int64_t cols, int x_dtype, int w_dtype, void* stream) {
-  Shape s;
-  if (int rc = validate("pt_rmsnorm_bwd", rows, cols, x_dtype, w_dtype, true, &s)) return rc;
-  hipStream_t st = as_stream(stream);
-  if (rows == 0) {
-    // Empty batch: the weight gradient is a sum over no rows.
-    if (dweight) return fill(dweight, cols, dtype_size(w_dtype), 0u, st);
-    return ok();
-  }
-  if (!dy || !x || !weight || !rstd) return fail(PT_EINVAL, "pt_rmsnorm_bwd: null pointer");
-  if (rows > 1 && (dy_row_stride < cols || x_row_stride < cols || (dx && dx_row_stride < cols)))
-    return fail(PT_EINVAL, "pt_rmsnorm_bwd: row stride smaller than cols");
-  const int vec = 16 / dtype_size(x_dtype);
-  BwdArgs a{};
-  a.aligned = (cols % vec == 0) && rows_aligned(x_dtype, dy, dy_row_stride) &&
-              rows_aligned(x_dtype, x, x_row_stride) &&
-              (dx == nullptr || rows_aligned(x_dtype, dx, dx_row_stride)) && aligned16(weight) &&
-              vector_weight(x_dtype, w_dtype);
-  a.shape = a.aligned ? s : unaligned_shape(cols, vec);
-  a.blocks = bwd_blocks(rows, a.shape);
-  float* partial = nullptr;
-  if (dweight) {
-    const size_t need = static_cast<size_t>(a.blocks) * static_cast<size_t>(cols) * sizeof(float);
-    if (!workspace || workspace_bytes < need)
-      return fail(PT_EINVAL,
-                  "pt_rmsnorm_bwd: workspace smaller than pt_rmsnorm_bwd_workspace_bytes()");
-    if (!aligned16(workspace)) return fail(PT_EINVAL, "pt_rmsnorm_bwd: workspace not aligned");
-    // LDS combining the row slots' weight-gradient sums holds one fp32 per column.
-    if (bwd_waves(a.shape) / a.shape.wpr > 1 && cols * 4 > 160 * 1024)
-      return fail(PT_EUNSUPPORTED, "pt_rmsnorm_bwd: hidden size too large for the LDS combine");
-    partial = static_cast<float*>(workspace);
-  }
-  a.dy = dy;
-  a.dys = dy_row_stride;
-  a.x = x;
-  a.xs = x_row_stride;
-  a.w = weight;
-  a.wdt = w_dtype;
-  a.rstd = rstd;
-  a.dx = dx;
-  a.dxs = dx_row_stride;
-  a.partial = partial;
-  a.rows = rows;
-  a.cols = static_cast<int>(cols);
-  a.xdt = x_dtype;
-  a.st = st;
-  bool launched;
-  if (x_dtype == PT_FLOAT32) {
-    launched = launch_bwd<float>(a);
-  } else if (x_dtype == PT_FLOAT16) {
-    launched = launch_bwd<_Float16>(a);
-  } else {
-    launched = launch_bwd<__bf16>(a);
-  }
-  if (!launched) return fail(PT_EUNSUPPORTED, "pt_rmsnorm_bwd: no kernel for this shape");
-  if (int rc = check_launch("pt_rmsnorm_bwd")) return rc;
-  if (dweight) {
-    const unsigned fblocks = static_cast<unsigned>((cols + kFinishCols - 1) / kFinishCols);
-    hipLaunchKernelGGL(rmsnorm_dw_finish_kernel, dim3(fblocks), dim3(256), 0, st, partial,
-                       a.blocks, static_cast<int>(cols), dweight, w_dtype);
-    return check_launch("pt_rmsnorm_bwd (dW finish)");
-  }
-  return ok();
+  return bwd_impl("pt_rmsnorm_bwd", dy, dy_row_stride, nullptr, 0, x, x_row_stride, weight, rstd,
+                  dx, dx_row_stride, dweight, workspace, workspace_bytes, rows, cols, x_dtype,
+                  w_dtype, stream);
+}
+
+int pt_residual_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* residual,
+                            int64_t residual_row_stride, const void* weight, void* h,
+                            int64_t h_row_stride, void* y, int64_t y_row_stride, float* rstd,
+                            int64_t rows, int64_t cols, float eps, int x_dtype, int w_dtype,
+                            void* stream) {
+  if (!residual || !h) return fail(PT_EINVAL, "pt_residual_rmsnorm_fwd: null pointer");
+  return fwd_impl("pt_residual_rmsnorm_fwd", x, x_row_stride, residual, residual_row_stride,
+                  weight, h, h_row_stride, y, y_row_stride, rstd, rows, cols, eps, x_dtype,
+                  w_dtype, stream);
+}
+
+int pt_residual_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* dh_in,
+                            int64_t dh_in_row_stride, const void* h, int64_t h_row_stride,
+                            const void* weight, const float* rstd, void* dh, int64_t dh_row_stride,
+                            void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
+                            int64_t cols, int x_dtype, int w_dtype, void* stream) {
+  if (!dh) return fail(PT_EINVAL, "pt_residual_rmsnorm_bwd: null pointer");
+  return bwd_impl("pt_residual_rmsnorm_bwd", dy, dy_row_stride, dh_in, dh_in_row_stride, h,
+                  h_row_stride, weight, rstd, dh, dh_row_stride, dweight, workspace,
+                  workspace_bytes, rows, cols, x_dtype, w_dtype, stream);
 }
 
 }  // extern "C"

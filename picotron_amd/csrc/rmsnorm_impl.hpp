@@ -151,6 +151,28 @@ struct RowRegs {
   }
 };
 
+// Stand-in for an absent row buffer (template variants without a residual stream).
+struct NoRegs {
+  __device__ __forceinline__ void opaque() {}
+};
+
+// Residual stream of the fused add + norm (decoder block: h = x + res, then norm(h)).
+template <typename T>
+struct ResidualIn {
+  const T* res;
+  int64_t res_stride;
+  T* h;
+  int64_t h_stride;
+};
+
+// Incoming gradient of h added to the norm's input gradient (h also feeds the block's
+// final residual add): dh = norm_backward(dy) + dh_in.
+template <typename T>
+struct ResidualGrad {
+  const T* dh_in;
+  int64_t dh_in_stride;
+};
+
 // Loads the lane's VPL vectors of a row.  Aligned path: branch-free and unmasked -- a
 // lane whose vector lies past the row end loads the row's first vector instead, and the
 // caller ignores it (in_row()).  Nothing may consume the loaded registers here: loads
@@ -221,11 +243,16 @@ __device__ __forceinline__ float row_sum(float v, float* red, int wave, int lane
 // reduced (PERSIST).  Weights are loaded once per wave, kept packed.  Without PERSIST the
 // kernel holds one row buffer only: fewer registers, more waves in flight per CU.
 
+// ADD: the fused residual add.  h = x + res is computed in fp32, rounded to the storage
+// type and written; the norm is taken of the rounded h, as the unfused graph normalises the
+// stored sum.
+
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT, bool PERSIST>
+          bool STORE_NT, bool PERSIST, bool ADD>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     const T* __restrict__ x, int64_t xs, const void* __restrict__ w, int wdt, T* __restrict__ y,
-    int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps, int iters) {
+    int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps, int iters,
+    ResidualIn<T> rin) {
   static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
@@ -244,8 +271,27 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
   LaneWeights<WT, VPL, V, ALIGNED> wv;
   wv.load(w, wdt, rl, LANES, cols);
 
-  auto process = [&](RowRegs<T, VPL>& xr, int64_t row, int buf) {
+  using ResRegs = std::conditional_t<ADD, RowRegs<T, VPL>, NoRegs>;
+  struct Row {
+    RowRegs<T, VPL> x;
+    ResRegs res;
+  };
+  auto process = [&](Row& rw, int64_t row, int buf) {
+    RowRegs<T, VPL>& xr = rw.x;
     const bool active = row < r1;
+    if constexpr (ADD) {
+      T* hr = rin.h + row * rin.h_stride;
+#pragma unroll
+      for (int k = 0; k < VPL; ++k) {
+        float o[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          xr.v[k].e[i] = Elem<T>::from_f32(xr.at(k, i) + rw.res.at(k, i));
+          o[i] = xr.at(k, i);
+        }
+        if (active) store_vec<T, LANES, ALIGNED, STORE_NT>(hr, rl, k, cols, o);
+      }
+    }
     float ss = 0.0f;
     if (active) {
 #pragma unroll
@@ -276,16 +322,19 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
 
   // Rows past the end are clamped to the last row for loading (keeping the loads
   // unconditional) and skipped by process().
-  auto load = [&](RowRegs<T, VPL>& xr, int64_t row) {
-    load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + (row < r1 ? row : r1 - 1) * xs, rl, cols, xr);
+  auto load = [&](Row& rw, int64_t row) {
+    const int64_t lr = row < r1 ? row : r1 - 1;
+    load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + lr * xs, rl, cols, rw.x);
+    if constexpr (ADD)
+      load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(rin.res + lr * rin.res_stride, rl, cols, rw.res);
   };
   int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
   if constexpr (!PERSIST) {
-    RowRegs<T, VPL> a;
+    Row a;
     load(a, ra);
     process(a, ra, 0);
   } else {
-    RowRegs<T, VPL> a, b;
+    Row a, b;
     load(a, ra);
     for (int it = 0; it < iters; it += 2) {
       const int64_t rb = ra + group_stride;
@@ -310,12 +359,17 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
 // block writes one fp32 partial row; the partial count (the grid) is fixed for a given
 // shape and tuning, so the weight gradient is reproducible.
 
+// ADD: dx = norm_backward(dy) + dh_in, summed in fp32 and rounded once (the fused residual
+// add's backward; dx may alias dh_in, each element being read before it is written by the
+// same lane).
+
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT, int PREFETCH = kBwdPrefetch>
+          bool STORE_NT, bool ADD, int PREFETCH = kBwdPrefetch>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, int64_t dys, const T* __restrict__ x, int64_t xs,
-    const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* __restrict__ dx,
-    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols, int iters) {
+    const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* dx,
+    int64_t dxs, float* __restrict__ partial, int64_t rows, int cols, int iters,
+    ResidualGrad<T> rg) {
   static_assert(WAVES % WPR == 0, "row slots must tile the block");
   constexpr int V = Elem<T>::VEC;
   constexpr int RPB = WAVES / WPR;
@@ -341,8 +395,10 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[k][i] = 0.0f;
 
+  using ResRegs = std::conditional_t<ADD, RowRegs<T, VPL>, NoRegs>;
   struct Buf {
     RowRegs<T, VPL> g, x;
+    ResRegs d;
     float r;
   };
   // Rows past the end are clamped to the last row for loading (keeping the loads
@@ -351,6 +407,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const int64_t lr = row < r1 ? row : r1 - 1;
     load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(dy + lr * dys, rl, cols, bf.g);
     load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(x + lr * xs, rl, cols, bf.x);
+    if constexpr (ADD)
+      load_row<T, VPL, LANES, ALIGNED, LOAD_NT>(rg.dh_in + lr * rg.dh_in_stride, rl, cols, bf.d);
     bf.r = rstd[lr];
   };
   auto process = [&](Buf& bf, int64_t row, int buf) {
@@ -367,6 +425,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     }
     bf.g.opaque();
     bf.x.opaque();
+    bf.d.opaque();
     dot = row_sum<WPR, WAVES>(dot, red, wave, lane, buf);
     if (!active) return;
     const float r = bf.r;
@@ -378,8 +437,10 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
       for (int k = 0; k < VPL; ++k) {
         float o[V];
 #pragma unroll
-        for (int i = 0; i < V; ++i)
+        for (int i = 0; i < V; ++i) {
           o[i] = r * (bf.g.at(k, i) * wv[k][i] - (bf.x.at(k, i) * r2) * dm);
+          if constexpr (ADD) o[i] += bf.d.at(k, i);
+        }
         store_vec<T, LANES, ALIGNED, STORE_NT>(dxr, rl, k, cols, o);
       }
     }
@@ -616,6 +677,11 @@ struct FwdArgs {
   Shape shape;
   int64_t blocks;
   hipStream_t st;
+  // fused residual add (res == nullptr: plain norm)
+  const void* res = nullptr;
+  int64_t res_s = 0;
+  void* h = nullptr;
+  int64_t h_s = 0;
 };
 
 struct BwdArgs {
@@ -636,27 +702,38 @@ struct BwdArgs {
   bool aligned;
   Shape shape;
   hipStream_t st;
+  // incoming gradient of h for the fused residual add (nullptr: plain norm backward)
+  const void* dh_in = nullptr;
+  int64_t dh_in_s = 0;
 };
 
 template <typename T, typename WT, bool ALIGNED>
 struct FwdLaunch {
   const FwdArgs& a;
+  template <int VPL, int WPR, bool PERSIST, bool ADD>
+  void go(int iters) const {
+    constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
+    const ResidualIn<T> rin{static_cast<const T*>(a.res), a.res_s, static_cast<T*>(a.h), a.h_s};
+    hipLaunchKernelGGL(
+        (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, PERSIST, ADD>),
+        dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
+        static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd, a.rows,
+        a.cols, a.eps, iters, rin);
+  }
   template <int VPL, int WPR>
   void run() const {
     constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
     const int iters = row_iters(a.rows, a.blocks, WAVES / WPR);
-    if (iters == 1) {
-      hipLaunchKernelGGL(
-          (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>),
-          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
-          static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd,
-          a.rows, a.cols, a.eps, iters);
+    if (a.res != nullptr) {
+      if (iters == 1) {
+        go<VPL, WPR, false, true>(iters);
+      } else {
+        go<VPL, WPR, true, true>(iters);
+      }
+    } else if (iters == 1) {
+      go<VPL, WPR, false, false>(iters);
     } else {
-      hipLaunchKernelGGL(
-          (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>),
-          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
-          static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd,
-          a.rows, a.cols, a.eps, iters);
+      go<VPL, WPR, true, false>(iters);
     }
   }
 };
@@ -670,11 +747,21 @@ struct BwdLaunch {
     constexpr int RPB = WAVES / WPR;
     const size_t lds =
         (RPB > 1 && a.partial != nullptr) ? static_cast<size_t>(a.cols) * sizeof(float) : 0;
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT>),
-                       dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
-                       static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs,
-                       a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
-                       a.cols, row_iters(a.rows, a.blocks, RPB));
+    const ResidualGrad<T> rg{static_cast<const T*>(a.dh_in), a.dh_in_s};
+    const int iters = row_iters(a.rows, a.blocks, RPB);
+    if (a.dh_in != nullptr) {
+      hipLaunchKernelGGL(
+          (rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>),
+          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
+          static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs, a.w, a.wdt,
+          a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows, a.cols, iters, rg);
+    } else {
+      hipLaunchKernelGGL(
+          (rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>),
+          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
+          static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs, a.w, a.wdt,
+          a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows, a.cols, iters, rg);
+    }
   }
 };
 

@@ -14,7 +14,7 @@ import warnings
 import torch
 from torch import Tensor, nn
 
-from picotron_amd.nn.triton_kernels.rmsnorm import triton_rms_norm
+from picotron_amd.nn.triton_kernels.rmsnorm import triton_residual_rms_norm, triton_rms_norm
 
 
 class RMSNorm(nn.Module):
@@ -29,18 +29,37 @@ class RMSNorm(nn.Module):
         self.use_triton_rmsnorm = use_triton_rmsnorm
         self._triton_fallback_warned = False
 
+    def _warn_fallback(self, error: Exception) -> None:
+        if not self._triton_fallback_warned:
+            warnings.warn(
+                f"Triton RMSNorm unavailable; using PyTorch fallback: {error}",
+                RuntimeWarning,
+                stacklevel=3,
+            )
+            self._triton_fallback_warned = True
+
+    def _eager(self, hidden_states: Tensor) -> Tensor:
+        variance = hidden_states.pow(2).mean(dim=-1, keepdim=True)
+        normalized = hidden_states * torch.rsqrt(variance + self.eps)
+        return normalized * self.weight
+
     def forward(self, hidden_states: Tensor) -> Tensor:
         if self.use_triton_rmsnorm:
             try:
                 return triton_rms_norm(hidden_states, self.weight, self.eps)
             except Exception as error:
-                if not self._triton_fallback_warned:
-                    warnings.warn(
-                        f"Triton RMSNorm unavailable; using PyTorch fallback: {error}",
-                        RuntimeWarning,
-                        stacklevel=2,
-                    )
-                    self._triton_fallback_warned = True
-        variance = hidden_states.pow(2).mean(dim=-1, keepdim=True)
-        normalized = hidden_states * torch.rsqrt(variance + self.eps)
-        return normalized * self.weight
+                self._warn_fallback(error)
+        return self._eager(hidden_states)
+
+    def add_and_norm(self, hidden_states: Tensor, residual: Tensor) -> tuple[Tensor, Tensor]:
+        """``(h, self(h))`` with ``h = hidden_states + residual``: the decoder block's residual
+        add and the norm after it (src/picotron/models/picotron_decoder.py:116-119), fused into
+        one kernel on the fast path."""
+
+        if self.use_triton_rmsnorm:
+            try:
+                return triton_residual_rms_norm(hidden_states, residual, self.weight, self.eps)
+            except Exception as error:
+                self._warn_fallback(error)
+        h = hidden_states + residual
+        return h, self._eager(h)

@@ -23,6 +23,7 @@ from picotron_amd.nn.triton_kernels.cross_entropy import (
 from picotron_amd.nn.triton_kernels.rmsnorm import (
     TritonRMSNormUnavailable,
     rms_norm_with_pytorch_forward,
+    triton_residual_rms_norm,
     triton_rms_norm,
 )
 from picotron_amd.nn.triton_kernels.rope import (
@@ -56,4 +57,5 @@ __all__ = [
     "triton_adamw_step",
     "triton_apply_rotary_embedding_pair",
     "triton_clip_grad_norm_and_step",
+    "triton_residual_rms_norm",
 ]

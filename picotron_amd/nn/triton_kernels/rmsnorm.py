@@ -8,6 +8,13 @@ validation behaviour.  The reference runs a Triton forward plus a separate PyTor
 (``pt_rmsnorm_fwd`` writes y and the fp32 rstd in one pass, ``pt_rmsnorm_bwd`` writes dx
 and a deterministic dW).  The PyTorch path (``use_fast_forward=False``) is the
 reference's own CPU-verifiable formula.
+
+``triton_residual_rms_norm(x, residual, weight, eps)`` fuses the decoder block's residual
+add with the norm that follows it (reference src/picotron/models/picotron_decoder.py:116-119:
+``hidden = hidden + attention(...)`` then ``mlp_norm(hidden)``): it returns ``(h, y)`` with
+``h = x + residual`` and ``y = RMSNorm(h)`` from one pass, and its backward adds the
+gradient arriving at ``h`` from the block's final residual add into the norm's input
+gradient in the same pass.
 """
 
 from __future__ import annotations
@@ -137,3 +144,56 @@ def rms_norm_with_pytorch_forward(hidden_states: Tensor, weight: Tensor, eps: fl
     same autograd Function (reference rmsnorm.py:163-171)."""
 
     return _RMSNormAutogradFunction.apply(hidden_states, weight, eps, False)
+
+
+class _ResidualRMSNormFunction(torch.autograd.Function):
+    """(h, y) = (x + residual, RMSNorm(x + residual)) with fused HIP forward and backward."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, residual: Tensor, weight: Tensor, eps: float):  # type: ignore[override]
+        h, y, rstd = ops.residual_rmsnorm_fwd(x, residual, weight, eps)
+        ctx.save_for_backward(h, weight, rstd)
+        ctx.set_materialize_grads(False)
+        return h, y
+
+    @staticmethod
+    def backward(ctx, grad_h: Tensor | None, grad_y: Tensor | None):  # type: ignore[override]
+        h, weight, rstd = ctx.saved_tensors
+        need_x, need_r, need_w = ctx.needs_input_grad[:3]
+        grad_w = None
+        if grad_y is None:
+            grad = grad_h
+        else:
+            try:
+                grad, grad_w = ops.residual_rmsnorm_bwd(grad_y, grad_h, h, weight, rstd, need_dw=need_w)
+            except _lib.HipKernelError as error:
+                global _backward_fallback_warned
+                if not _backward_fallback_warned:
+                    warnings.warn(
+                        f"HIP RMSNorm backward unavailable; using PyTorch fallback: {error}",
+                        RuntimeWarning,
+                        stacklevel=2,
+                    )
+                    _backward_fallback_warned = True
+                grad, grad_w = _pytorch_backward(h, weight, rstd.unsqueeze(-1), grad_y)
+                if grad_h is not None:
+                    grad = (grad.float() + grad_h.float()).to(h.dtype)
+        return (grad if need_x else None), (grad if need_r else None), (grad_w if need_w else None), None
+
+
+def triton_residual_rms_norm(
+    hidden_states: Tensor, residual: Tensor, weight: Tensor, eps: float
+) -> tuple[Tensor, Tensor]:
+    """``h = hidden_states + residual`` and ``RMSNorm(h)`` fused; returns ``(h, y)``.
+
+    Raises :class:`TritonRMSNormUnavailable` when the fused path cannot run (callers then
+    add and normalise with PyTorch).
+    """
+
+    _validate_triton_inputs(hidden_states, weight)
+    require_hip(TritonRMSNormUnavailable, "RMSNorm", residual)
+    if residual.shape != hidden_states.shape or residual.dtype != hidden_states.dtype:
+        raise TritonRMSNormUnavailable("residual must match hidden_states in shape and dtype.")
+    if not residual.is_contiguous():
+        raise TritonRMSNormUnavailable("HIP RMSNorm requires contiguous inputs.")
+    return _ResidualRMSNormFunction.apply(hidden_states, residual, weight, eps)

@@ -134,6 +134,85 @@ def rmsnorm_bwd(
     return dx, dw
 
 
+def residual_rmsnorm_fwd(
+    x: Tensor, residual: Tensor, weight: Tensor, eps: float
+) -> tuple[Tensor, Tensor, Tensor]:
+    """h = x + residual (rounded to x's dtype) and y = RMSNorm(h) in one pass; returns
+    (h, y, rstd fp32)."""
+
+    device = _check_cuda(x, residual, weight)
+    cols = x.size(-1)
+    if residual.shape != x.shape or residual.dtype != x.dtype:
+        raise ValueError("residual must match x in shape and dtype")
+    if weight.dim() != 1 or weight.numel() != cols:
+        raise ValueError("RMSNorm weight must be 1-D with hidden-size elements")
+    weight = weight.contiguous()
+    x2 = _as_rows(x, cols)
+    r2 = _as_rows(residual, cols)
+    rows = x2.size(0)
+    h = torch.empty(x.shape, dtype=x.dtype, device=device)
+    y = torch.empty(x.shape, dtype=x.dtype, device=device)
+    rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=device)
+    _lib.call(
+        "pt_residual_rmsnorm_fwd",
+        x2.data_ptr(), x2.stride(0) if rows > 1 else cols, r2.data_ptr(),
+        r2.stride(0) if rows > 1 else cols, weight.data_ptr(), h.data_ptr(), cols, y.data_ptr(), cols,
+        rstd.data_ptr(), rows, cols, float(eps), dtype_code(x.dtype), dtype_code(weight.dtype),
+        _stream(device),
+    )
+    return h, y, rstd
+
+
+def residual_rmsnorm_bwd(
+    dy: Tensor,
+    dh_in: Tensor | None,
+    h: Tensor,
+    weight: Tensor,
+    rstd: Tensor,
+    need_dw: bool = True,
+    out: Tensor | None = None,
+) -> tuple[Tensor, Tensor | None]:
+    """dh = RMSNorm-backward(dy) + dh_in (in h's dtype) and the weight gradient.  ``out``
+    (may be ``dh_in`` itself) receives dh when given."""
+
+    device = _check_cuda(dy, h, weight, rstd)
+    cols = h.size(-1)
+    if dy.dtype != h.dtype:
+        dy = dy.to(h.dtype)
+    weight = weight.contiguous()
+    rstd = rstd.contiguous()
+    h2 = _as_rows(h, cols)
+    dy2 = _as_rows(dy, cols)
+    rows = h2.size(0)
+    if rstd.numel() != rows or rstd.dtype != torch.float32:
+        raise ValueError("rstd must hold one fp32 value per row")
+    d2 = None
+    if dh_in is not None:
+        if dh_in.shape != h.shape:
+            raise ValueError("dh_in must match h")
+        if dh_in.dtype != h.dtype:
+            dh_in = dh_in.to(h.dtype)
+        d2 = _as_rows(dh_in, cols)
+    if out is None:
+        out = torch.empty(h.shape, dtype=h.dtype, device=device)
+    elif out.shape != h.shape or out.dtype != h.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor like h")
+    dw = torch.empty(cols, dtype=weight.dtype, device=device) if need_dw else None
+    ws, ws_bytes = None, 0
+    if need_dw:
+        ws_bytes = _lib.lib().pt_rmsnorm_bwd_workspace_bytes(rows, cols, dtype_code(h.dtype))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
+    _lib.call(
+        "pt_residual_rmsnorm_bwd",
+        dy2.data_ptr(), dy2.stride(0) if rows > 1 else cols, _ptr(d2),
+        (d2.stride(0) if rows > 1 else cols) if d2 is not None else 0, h2.data_ptr(),
+        h2.stride(0) if rows > 1 else cols, weight.data_ptr(), rstd.data_ptr(), out.data_ptr(), cols,
+        _ptr(dw), _ptr(ws), ws_bytes, rows, cols, dtype_code(h.dtype), dtype_code(weight.dtype),
+        _stream(device),
+    )
+    return out, dw
+
+
 # ------------------------------------------------------------------ SwiGLU
 
 

@@ -333,3 +333,34 @@ def test_clip_grad_norm_oracle_matches_torch_library(max_norm):
     if max_norm > 1e3:  # below the norm: the coefficient clamps to exactly 1
         for c, g in zip(clipped, grads):
             assert torch.equal(c, g)
+
+
+def test_residual_rmsnorm_oracle_matches_torch_autograd_of_the_block():
+    # h = x + r feeds both the norm and a later residual add (out = h + mlp(norm(h)));
+    # torch's autograd of that graph gives dx = dr = dh_in + d norm / d h
+    torch.manual_seed(12)
+    x = torch.randn(3, 5, 16, dtype=torch.float64, requires_grad=True)
+    r = torch.randn(3, 5, 16, dtype=torch.float64, requires_grad=True)
+    w = (1 + 0.02 * torch.randn(16, dtype=torch.float64)).requires_grad_(True)
+    eps = 1e-5
+    h = x + r
+    y = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps) * w
+    dy = torch.randn_like(y)
+    dh_in = torch.randn_like(h)
+    torch.autograd.backward([y, h], [dy, dh_in])
+    oh, oy, _ = o_rms.residual_forward(x.detach(), r.detach(), w.detach(), eps)
+    torch.testing.assert_close(oh, h.detach(), rtol=0, atol=0)
+    torch.testing.assert_close(oy, y.detach(), rtol=1e-12, atol=1e-12)
+    dh, dw = o_rms.residual_backward(dy, dh_in, oh, w.detach(), eps)
+    torch.testing.assert_close(dh, x.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dh, r.grad, rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(dw, w.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_residual_rmsnorm_oracle_rounds_h_like_torch():
+    torch.manual_seed(13)
+    x = torch.randn(64, 32).bfloat16()
+    r = torch.randn(64, 32).bfloat16()
+    h, _, _ = o_rms.residual_forward(x, r, torch.ones(32), 1e-6)
+    assert h.dtype == torch.bfloat16
+    assert torch.equal(h, x + r)  # torch's bf16 add: fp32 sum rounded once

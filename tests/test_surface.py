@@ -174,6 +174,16 @@ def test_shifted_cross_entropy_cpu_fallback_is_the_train_loop_expression():
     torch.testing.assert_close(plain(logits, ids, shift=True), actual)
 
 
+def test_rmsnorm_add_and_norm_cpu_fallback():
+    torch.manual_seed(5)
+    x, r = torch.randn(2, 3, 8), torch.randn(2, 3, 8)
+    norm = RMSNorm(8, eps=1e-6, use_triton_rmsnorm=True)
+    with pytest.warns(RuntimeWarning, match="Triton RMSNorm unavailable"):
+        h, y = norm.add_and_norm(x, r)
+    torch.testing.assert_close(h, x + r, rtol=0, atol=0)
+    torch.testing.assert_close(y, RMSNorm(8, eps=1e-6)(x + r), rtol=0, atol=0)
+
+
 def test_adamw_clip_fallback_is_clip_grad_norm_then_step():
     torch.manual_seed(4)
     ref_params = [torch.nn.Parameter(torch.randn(5)), torch.nn.Parameter(torch.randn(3, 2))]
