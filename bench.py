@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|zero_step|copy]
 
 Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
 (8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
@@ -731,6 +731,81 @@ class AdamWClipWorkload(AdamWWorkload):
         )
 
 
+class ZeroMixedPrecisionStepWorkload(AdamWWorkload):
+    """The ZeRO mixed-precision update on one rank (reference src/picotron/parallel/zero.py:
+    DistributedGradScaler.step :50-79 -> unscale_and_check_ :139-163 -> clip_grad_norm_
+    :165-186 -> the inner AdamW step), fused."""
+
+    name = "zero_step"
+    metric = "Fused unscale + inf-check + clip + AdamW step HBM GB/s & % of peak, 1.2e9 fp32 params"
+    loss_scale = 65536.0
+
+    def __init__(self, layers: int) -> None:
+        super().__init__(layers)
+        from picotron_amd.nn.triton_kernels import triton_unscale_clip_and_step
+
+        n = self.n
+        self.fn = triton_unscale_clip_and_step
+        self.g.mul_(self.loss_scale)  # gradients as the scaled loss's backward leaves them
+        self.g_scaled = self.g.clone()
+        self.prm = torch.nn.Parameter(self.p)
+        self.prm.grad = self.g
+        self.opt = torch.optim.AdamW([self.prm], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        self.bytes_per_step = 36 * n  # stats: read g; step: read p, g, m, v, write p, m, v, g
+        self.dominant = ("fused unscale + clip + step (grad_stats_kernel + grad_stats_finish_kernel, one "
+                         "host read of the overflow flag, adamw_kernel with the combined multiplier)")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "ZeRO-1 mixed-precision update on one rank: loss scale 65536, finite check, unscale, "
+            "clip_grad_norm_(1.0) with the ZeRO rule (scale only if coef < 1) and the AdamW step, one "
+            "flat 1.2e9-element fp32 parameter; step = triton_unscale_clip_and_step (each step "
+            "unscales the gradients the previous one left; the values do not change the traffic)"
+        )
+
+    def _rescale(self):
+        self.g.copy_(self.g_scaled)
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        found = self.fn(self.opt, self.loss_scale, 1.0)
+        if events is not None:
+            end.record()
+        if found:
+            raise RuntimeError("unexpected overflow in the synthetic gradients")
+
+    def extra(self, steps: int) -> dict:
+        """The reference sequence on the same data: per-parameter finite check (host sync),
+        g *= 1/scale, squared norm (host sync on the coefficient), g *= coef, then the fused
+        step (torch's own AdamW step is slower still)."""
+
+        def reference():
+            self._rescale()
+            g = self.prm.grad
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            if not bool(torch.isfinite(g).all()):
+                raise RuntimeError("unexpected overflow")
+            g.mul_(1.0 / self.loss_scale)
+            sq = torch.zeros((), device=g.device, dtype=torch.float32)
+            sq.add_(g.float().pow(2).sum())
+            coef = 1.0 / (sq.sqrt() + 1e-6)
+            if coef < 1:
+                g.mul_(coef.to(dtype=g.dtype))
+            from picotron_amd.nn.triton_kernels import triton_adamw_step
+            triton_adamw_step(self.opt)
+            torch.cuda.synchronize()
+            return time.perf_counter() - t0
+
+        reference()
+        total = sum(reference() for _ in range(steps))
+        return {"reference_sequence_ms_per_step": round(total / steps * 1e3, 4)}
+
+    def cpu_baseline(self) -> dict:
+        return None
+
+
 class CopyWorkload(Workload):
     name = "copy"
     metric = "128-bit streaming copy HBM GB/s (achievable-bandwidth reference)"
@@ -773,11 +848,12 @@ WORKLOADS = {
     "ce_train": CrossEntropyTrainWorkload,
     "adamw": AdamWWorkload,
     "adamw_clip": AdamWClipWorkload,
+    "zero_step": ZeroMixedPrecisionStepWorkload,
     "copy": CopyWorkload,
 }
 
 DEFAULT_LAYERS = {"rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
-                  "copy": 4}
+                  "zero_step": 1, "copy": 4}
 
 
 def _traffic(workload: str) -> dict | None:
@@ -834,7 +910,7 @@ def main() -> int:
     # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
     # records add a few microseconds per launch, so this pass is not used for the value.
     per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
-                "adamw_clip": 1, "copy": layers}[args.workload]
+                "adamw_clip": 1, "zero_step": 1, "copy": layers}[args.workload]
     events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(args.steps * per_step)]
     pending = list(reversed(events))

@@ -239,6 +239,30 @@ int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_
                          double beta1, double beta2, double eps, double weight_decay, double step,
                          const float* grad_scale, int write_grad, void* stream);
 
+/* Mixed-precision / ZeRO gradient handling before the step
+ * (src/picotron/parallel/zero.py:139-163 unscale_and_check_: a finite check of every
+ * gradient, one host sync per parameter, then g *= 1/scale; :165-186 clip_grad_norm_:
+ * squared norm in fp32, g *= coef when coef < 1).  One read of every gradient:
+ *   pt_grad_stats: total_norm = ||g * inv_scale||_2 (inv_scale: device fp32, NULL = 1),
+ *     found_inf = 1 if any g is inf or NaN, and grad_scale = inv_scale * coefficient, where
+ *     for max_norm >= 0 coefficient c = (1 / (total_norm + 1e-6)) * max_norm is applied as
+ *     min(c, 1) (clip_mode 0: torch.nn.utils.clip_grad_norm_) or as c if c < 1 else 1
+ *     (clip_mode 1: the ZeRO optimizer), and is 1 for max_norm < 0.  Outputs are device
+ *     scalars; workspace pt_grad_stats_workspace_bytes(total_blocks).  The caller reads
+ *     found_inf (one sync for all tensors) and either skips the step or passes grad_scale
+ *     to pt_adamw_step_scaled -- unscale, clip and step in one more pass -- or to
+ *     pt_grad_scale.
+ *   pt_grad_scale: g *= *scale in place for every gradient of the table (no memory traffic
+ *     when *scale is exactly 1).
+ * Tables have the pt_adamw_step layout (only grad address, numel, first block read). */
+size_t pt_grad_stats_workspace_bytes(int64_t total_blocks);
+int pt_grad_stats(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                  const float* inv_scale, double max_norm, int clip_mode, float* total_norm_out,
+                  float* grad_scale_out, int32_t* found_inf_out, void* workspace,
+                  size_t workspace_bytes, void* stream);
+int pt_grad_scale(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                  const float* scale, void* stream);
+
 /* ---------------------------------------------------------------- Utility
  * Device-to-device copy of `bytes` (multiple of 16, 16-byte aligned pointers) with the
  * same 128-bit load/store pattern as the streaming kernels.  No reference counterpart:

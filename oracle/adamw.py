@@ -58,3 +58,29 @@ def clip_grad_norm(grads: list[Tensor], max_norm: float, compute: torch.dtype = 
     total = torch.sqrt(sum((g * g).sum() for g in gs))
     coef = torch.clamp(max_norm / (total + 1e-6), max=1.0)
     return total, [g * coef for g in gs]
+
+
+def unscale_and_check(grads: list[Tensor], scale: float) -> tuple[bool, list[Tensor]]:
+    """The ZeRO optimizer's unscale_and_check_ (reference src/picotron/parallel/zero.py:139-163)
+    on one rank: (True, grads unchanged) if any gradient holds inf or NaN, else
+    (False, every gradient multiplied by the Python float 1/scale in its own dtype)."""
+
+    if any(not bool(torch.isfinite(g).all()) for g in grads):
+        return True, list(grads)
+    inverse_scale = 1.0 / scale
+    return False, [g * inverse_scale for g in grads]
+
+
+def zero_clip_grad_norm(grads: list[Tensor], max_norm: float, compute: torch.dtype = torch.float64) -> tuple[Tensor, list[Tensor]]:
+    """The ZeRO optimizer's clip_grad_norm_ (reference src/picotron/parallel/zero.py:165-186)
+    on one rank: total = ||all grads||_2, coef = max_norm / (total + 1e-6), gradients
+    multiplied by coef only when coef < 1.  Returns (total, grads) in ``compute``."""
+
+    gs = [g.to(compute) for g in grads]
+    if not gs:
+        return torch.zeros((), dtype=compute), []
+    total = torch.sqrt(sum((g * g).sum() for g in gs))
+    coef = max_norm / (total + 1e-6)
+    if bool(coef < 1):
+        gs = [g * coef for g in gs]
+    return total, gs

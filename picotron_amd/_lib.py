@@ -103,6 +103,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int64, c_double, c_double, c_double, c_double, c_double, c_double,
          c_void_p, c_int, c_void_p],
     ),
+    "pt_grad_stats_workspace_bytes": (c_size_t, [c_int64]),
+    "pt_grad_stats": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_double, c_int, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_size_t, c_void_p],
+    ),
+    "pt_grad_scale": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "pt_copy": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
 }
 

@@ -133,18 +133,24 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
   }
 }
 
-// Per-block partial sum of squares of the gradients (table layout as the step; only the
-// g, n and first_block fields are read).
-__global__ __launch_bounds__(kThreads) void grad_sumsq_kernel(const AdamRec* __restrict__ table,
+// Per-block statistics of the gradients (table layout as the step; only the g, n and
+// first_block fields are read): the partial sum of squares of u = g * inv_scale (the
+// unscaled gradient, inv_scale = 1 when absent) and, when `nonfinite` is given, whether any
+// g of the block is inf or NaN.
+__global__ __launch_bounds__(kThreads) void grad_stats_kernel(const AdamRec* __restrict__ table,
                                                               int64_t ntensors,
-                                                              float* __restrict__ partial) {
+                                                              const float* __restrict__ inv_scale,
+                                                              float* __restrict__ partial,
+                                                              int* __restrict__ nonfinite) {
   __shared__ float red[kThreads / 64];
   const int64_t blk = blockIdx.x;
   const AdamRec r = table[find_tensor(table, ntensors, blk)];
   const int64_t start = (blk - r.first_block) * kBlockElems;
   const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
   const float* G = reinterpret_cast<const float*>(r.g);
+  const float s = inv_scale != nullptr ? *inv_scale : 1.0f;
   float acc = 0.0f;
+  bool bad = false;
   if ((r.g & 15) == 0 && end - start == kBlockElems) {
     f32x4 gv[kUnroll];
 #pragma unroll
@@ -154,11 +160,20 @@ __global__ __launch_bounds__(kThreads) void grad_sumsq_kernel(const AdamRec* __r
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc += gv[k][j] * gv[k][j];
+      for (int j = 0; j < 4; ++j) {
+        const float u = gv[k][j] * s;
+        acc += u * u;
+        bad |= !__builtin_isfinite(gv[k][j]);
+      }
   } else {
-    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) acc += G[i] * G[i];
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
+      const float u = G[i] * s;
+      acc += u * u;
+      bad |= !__builtin_isfinite(G[i]);
+    }
   }
   acc = wave_sum(acc);
+  const int any_bad = __syncthreads_or(bad ? 1 : 0);
   if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -166,22 +181,33 @@ __global__ __launch_bounds__(kThreads) void grad_sumsq_kernel(const AdamRec* __r
 #pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) t += red[w];
     partial[blk] = t;
+    if (nonfinite != nullptr) nonfinite[blk] = any_bad;
   }
 }
 
-// total_norm = sqrt(sum of the partials, added in double in a fixed order) and torch's
-// clip coefficient, both as fp32 device scalars:
-//   clip_coef = (1 / (total_norm + 1e-6)) * max_norm   (Python's max_norm / tensor)
-//   clip_coef_clamped = clamp(clip_coef, max=1)          (NaN stays NaN)
-__global__ __launch_bounds__(1024) void grad_norm_finish_kernel(const float* __restrict__ partial,
-                                                                int64_t nblocks, float max_norm,
-                                                                float* __restrict__ total_out,
-                                                                float* __restrict__ coef_out) {
+// total_norm = sqrt(sum of the partials, added in double in a fixed order), the gradient
+// multiplier and the non-finite flag, as device scalars.  With max_norm >= 0 the clip
+// coefficient is computed as both clipping routines compute it,
+//   c = (1 / (total_norm + 1e-6)) * max_norm   (Python's max_norm / tensor),
+// and applied as torch.nn.utils.clip_grad_norm_ does (CLIP_CLAMP: min(c, 1), NaN stays NaN)
+// or as picotron's ZeRO optimizer does (CLIP_IF_BELOW_ONE: c if c < 1 else 1).  The
+// multiplier is inv_scale * coefficient (inv_scale = 1 when absent).
+enum ClipMode { CLIP_CLAMP = 0, CLIP_IF_BELOW_ONE = 1 };
+
+__global__ __launch_bounds__(1024) void grad_stats_finish_kernel(
+    const float* __restrict__ partial, const int* __restrict__ nonfinite, int64_t nblocks,
+    float max_norm, int clip_mode, const float* __restrict__ inv_scale,
+    float* __restrict__ total_out, float* __restrict__ scale_out, int* __restrict__ found_out) {
   __shared__ double red[16];
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < nblocks; i += 1024) acc += static_cast<double>(partial[i]);
+  int bad = 0;
+  for (int64_t i = threadIdx.x; i < nblocks; i += 1024) {
+    acc += static_cast<double>(partial[i]);
+    if (nonfinite != nullptr) bad |= nonfinite[i];
+  }
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
+  const int any_bad = __syncthreads_or(bad);
   if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -189,10 +215,46 @@ __global__ __launch_bounds__(1024) void grad_norm_finish_kernel(const float* __r
 #pragma unroll
     for (int w = 0; w < 16; ++w) t += red[w];
     const float total = static_cast<float>(sqrt(t));
-    const float denom = total + 1e-6f;
-    const float coef = (1.0f / denom) * max_norm;
+    float coef = 1.0f;
+    if (max_norm >= 0.0f) {
+      const float c = (1.0f / (total + 1e-6f)) * max_norm;
+      coef = clip_mode == CLIP_CLAMP ? (c > 1.0f ? 1.0f : c) : (c < 1.0f ? c : 1.0f);
+    }
     *total_out = total;
-    *coef_out = coef > 1.0f ? 1.0f : coef;
+    *scale_out = (inv_scale != nullptr ? *inv_scale : 1.0f) * coef;
+    if (found_out != nullptr) *found_out = any_bad;
+  }
+}
+
+// In-place g *= *scale over every gradient of the table; nothing at all when the scale is
+// exactly 1 (a clip that does not clip).  A grid of a few blocks per CU walks the table's
+// blocks, so that case costs one small launch.
+__global__ __launch_bounds__(kThreads) void grad_scale_kernel(const AdamRec* __restrict__ table,
+                                                              int64_t ntensors, int64_t nblocks,
+                                                              const float* __restrict__ scale) {
+  const float s = *scale;
+  if (s == 1.0f) return;
+  for (int64_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+    const AdamRec r = table[find_tensor(table, ntensors, blk)];
+    const int64_t start = (blk - r.first_block) * kBlockElems;
+    const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
+    float* G = reinterpret_cast<float*>(r.g);
+    if ((r.g & 15) == 0 && end - start == kBlockElems) {
+      f32x4 gv[kUnroll];
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k)
+        gv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
+            G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
+#pragma unroll
+      for (int k = 0; k < kUnroll; ++k) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gv[k][j] = gv[k][j] * s;
+        __builtin_nontemporal_store(gv[k], reinterpret_cast<f32x4*>(
+            G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
+      }
+    } else {
+      for (int64_t i = start + threadIdx.x; i < end; i += kThreads) G[i] = G[i] * s;
+    }
   }
 }
 
@@ -268,29 +330,84 @@ size_t pt_clip_grad_norm_workspace_bytes(int64_t total_blocks) {
   return total_blocks < 0 ? 0 : static_cast<size_t>(total_blocks) * sizeof(float);
 }
 
+size_t pt_grad_stats_workspace_bytes(int64_t total_blocks) {
+  return total_blocks < 0 ? 0 : static_cast<size_t>(total_blocks) * (sizeof(float) + sizeof(int));
+}
+
+}  // extern "C"
+
+namespace {
+
+// Launches the statistics pass and its finish.  `nonfinite` (blocks ints) may be null.
+int grad_stats_run(const char* fn, const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                   const float* inv_scale, double max_norm, int clip_mode, float* total_out,
+                   float* scale_out, int* found_out, float* partial, int* nonfinite,
+                   hipStream_t st) {
+  int rc = check_table(fn, table, n_tensors, total_blocks);
+  if (rc != -1 && rc != PT_OK) return rc;
+  if (rc == PT_OK) {
+    hipLaunchKernelGGL(grad_stats_kernel, dim3(static_cast<unsigned>(total_blocks)),
+                       dim3(kThreads), 0, st, reinterpret_cast<const AdamRec*>(table), n_tensors,
+                       inv_scale, partial, nonfinite);
+    if (int lrc = check_launch(fn)) return lrc;
+  } else {
+    total_blocks = 0;  // no gradients: the norm of nothing is 0
+  }
+  hipLaunchKernelGGL(grad_stats_finish_kernel, dim3(1), dim3(1024), 0, st, partial, nonfinite,
+                     total_blocks, static_cast<float>(max_norm), clip_mode, inv_scale, total_out,
+                     scale_out, found_out);
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" {
+
 int pt_clip_grad_norm(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
                       double max_norm, float* total_norm_out, float* clip_coef_out,
                       void* workspace, size_t workspace_bytes, void* stream) {
   if (!total_norm_out || !clip_coef_out)
     return fail(PT_EINVAL, "pt_clip_grad_norm: null output");
-  hipStream_t st = as_stream(stream);
-  int rc = check_table("pt_clip_grad_norm", table, n_tensors, total_blocks);
-  if (rc != -1 && rc != PT_OK) return rc;
-  if (rc == PT_OK) {
-    if (!workspace || workspace_bytes < pt_clip_grad_norm_workspace_bytes(total_blocks) ||
-        !aligned16(workspace))
-      return fail(PT_EINVAL, "pt_clip_grad_norm: workspace too small or not 16-byte aligned");
-    hipLaunchKernelGGL(grad_sumsq_kernel, dim3(static_cast<unsigned>(total_blocks)),
-                       dim3(kThreads), 0, st, reinterpret_cast<const AdamRec*>(table), n_tensors,
-                       static_cast<float*>(workspace));
-    if (int lrc = check_launch("pt_clip_grad_norm")) return lrc;
-  } else {
-    total_blocks = 0;  // no gradients: the norm of nothing is 0
-  }
-  hipLaunchKernelGGL(grad_norm_finish_kernel, dim3(1), dim3(1024), 0, st,
-                     static_cast<const float*>(workspace), total_blocks,
-                     static_cast<float>(max_norm), total_norm_out, clip_coef_out);
-  return check_launch("pt_clip_grad_norm");
+  if (!(max_norm >= 0.0)) return fail(PT_EINVAL, "pt_clip_grad_norm: max_norm must be >= 0");
+  if (n_tensors > 0 && total_blocks > 0 &&
+      (!workspace || workspace_bytes < pt_clip_grad_norm_workspace_bytes(total_blocks) ||
+       !aligned16(workspace)))
+    return fail(PT_EINVAL, "pt_clip_grad_norm: workspace too small or not 16-byte aligned");
+  return grad_stats_run("pt_clip_grad_norm", table, n_tensors, total_blocks, nullptr, max_norm,
+                        CLIP_CLAMP, total_norm_out, clip_coef_out, nullptr,
+                        static_cast<float*>(workspace), nullptr, as_stream(stream));
+}
+
+int pt_grad_stats(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                  const float* inv_scale, double max_norm, int clip_mode, float* total_norm_out,
+                  float* grad_scale_out, int32_t* found_inf_out, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  if (!total_norm_out || !grad_scale_out || !found_inf_out)
+    return fail(PT_EINVAL, "pt_grad_stats: null output");
+  if (clip_mode != CLIP_CLAMP && clip_mode != CLIP_IF_BELOW_ONE)
+    return fail(PT_EINVAL, "pt_grad_stats: unknown clip mode");
+  if (n_tensors > 0 && total_blocks > 0 &&
+      (!workspace || workspace_bytes < pt_grad_stats_workspace_bytes(total_blocks) ||
+       !aligned16(workspace)))
+    return fail(PT_EINVAL, "pt_grad_stats: workspace too small or not 16-byte aligned");
+  float* partial = static_cast<float*>(workspace);
+  int* nonfinite = partial != nullptr ? reinterpret_cast<int*>(partial + total_blocks) : nullptr;
+  return grad_stats_run("pt_grad_stats", table, n_tensors, total_blocks, inv_scale, max_norm,
+                        clip_mode, total_norm_out, grad_scale_out, found_inf_out, partial,
+                        nonfinite, as_stream(stream));
+}
+
+int pt_grad_scale(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                  const float* scale, void* stream) {
+  const int rc = check_table("pt_grad_scale", table, n_tensors, total_blocks);
+  if (rc == -1) return ok();
+  if (rc != PT_OK) return rc;
+  if (!scale) return fail(PT_EINVAL, "pt_grad_scale: null scale");
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
+  const unsigned grid = static_cast<unsigned>(total_blocks < cap ? total_blocks : cap);
+  hipLaunchKernelGGL(grad_scale_kernel, dim3(grid), dim3(kThreads), 0, as_stream(stream),
+                     reinterpret_cast<const AdamRec*>(table), n_tensors, total_blocks, scale);
+  return check_launch("pt_grad_scale");
 }
 
 }  // extern "C"

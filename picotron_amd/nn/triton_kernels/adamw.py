@@ -186,6 +186,120 @@ def triton_clip_grad_norm_and_step(
     return total_norm
 
 
+# ------------------------------------------------------------------ loss scaling and ZeRO
+#
+# The mixed-precision / ZeRO path of the reference (src/picotron/parallel/zero.py) handles
+# gradients outside the optimizer: DistributedGradScaler.step (:50-79) calls
+# ZeroOptimizer.unscale_and_check_ (:139-163; a finite check per parameter, each a host
+# sync, then g *= 1/scale), ZeroOptimizer.clip_grad_norm_ (:165-186; g *= coef when coef < 1)
+# and the inner torch AdamW step (:130-137).  The functions below run that on one rank
+# with one read of the gradients for all statistics and a single host sync.
+
+
+def _grads_of(parameters) -> tuple[list[Tensor], torch.device | None]:
+    grads = [p.grad for p in parameters if p.grad is not None]
+    device = None
+    for g in grads:
+        if not g.is_cuda or g.dtype != torch.float32 or g.is_sparse or not g.is_contiguous():
+            raise _reject("gradients that are not dense contiguous fp32 GPU tensors")
+        if device is None:
+            device = g.device
+        elif g.device != device:
+            raise _reject("gradients on several devices")
+    if device is not None:
+        reason = _lib.unavailable_reason()
+        if reason is not None:
+            raise TritonAdamWUnavailable(f"HIP kernel library unavailable: {reason}")
+        if not ops.device_supported(device.index if device.index is not None else torch.cuda.current_device()):
+            raise _reject("devices other than gfx950")
+    return grads, device
+
+
+def _grad_table(grads: list[Tensor], device: torch.device) -> tuple[Tensor, int]:
+    host_table, blocks = ops.adamw_table(grads, grads, grads, grads)
+    if blocks * 256 > 0xFFFFFFFF:
+        raise _reject("more than 2^24 blocks of gradient elements")
+    return _device_table(host_table, device), blocks
+
+
+def triton_unscale_and_check_(parameters, scale: float) -> bool:
+    """``ZeroOptimizer.unscale_and_check_`` on one rank: True (gradients untouched) if any
+    gradient is inf or NaN, else every gradient is multiplied by ``1 / scale`` and False."""
+
+    if scale <= 0:
+        raise ValueError("loss scale must be positive.")
+    grads, device = _grads_of(parameters)
+    if device is None:
+        return False
+    table, blocks = _grad_table(grads, device)
+    inv = torch.tensor(1.0 / scale, dtype=torch.float32, device=device)
+    _, multiplier, found_inf = ops.grad_stats(table, blocks, inv)
+    if bool(found_inf.item()):
+        return True
+    ops.grad_scale(table, blocks, multiplier)
+    return False
+
+
+def triton_zero_clip_grad_norm_(parameters, max_norm: float) -> Tensor:
+    """``ZeroOptimizer.clip_grad_norm_`` on one rank: returns the total norm and multiplies
+    every gradient by ``max_norm / (total_norm + 1e-6)`` when that is below 1, without a
+    host sync (the comparison happens on the device)."""
+
+    if max_norm <= 0:
+        raise ValueError("max_norm must be positive.")
+    grads, device = _grads_of(parameters)
+    if device is None:
+        return torch.tensor(0.0)
+    table, blocks = _grad_table(grads, device)
+    total, multiplier, _ = ops.grad_stats(table, blocks, None, max_norm, ops.CLIP_IF_BELOW_ONE)
+    ops.grad_scale(table, blocks, multiplier)
+    return total
+
+
+def triton_unscale_clip_and_step(
+    optimizer: Optimizer, scale: float, max_norm: float | None = None, *, parameters=None
+) -> bool:
+    """The ZeRO mixed-precision update on one rank, fused: ``unscale_and_check_(scale)``,
+    then (if every gradient is finite) ``clip_grad_norm_(max_norm)`` and the AdamW step of
+    ``optimizer`` (the ZeRO optimizer's inner ``torch.optim.AdamW``).
+
+    One pass reads every gradient of ``parameters`` (default: the optimizer's) for the
+    finite check, the norm of the unscaled gradients and the combined unscale x clip
+    multiplier; one host sync reads the finite flag; the step then applies the multiplier
+    as it reads each gradient and writes the unscaled, clipped gradient back.  Gradients of
+    ``parameters`` outside the optimizer are rescaled in place as the reference does.
+    Returns True (nothing changed) when a gradient is inf or NaN, like
+    ``unscale_and_check_``.
+    """
+
+    if scale <= 0:
+        raise ValueError("loss scale must be positive.")
+    if max_norm is not None and max_norm <= 0:
+        raise ValueError("max_norm must be positive.")
+    groups, device = _plan(optimizer)
+    owned = [p for _, params in groups for p in params]
+    if parameters is None:
+        parameters = owned
+    grads, gdevice = _grads_of(parameters)
+    if gdevice is None:
+        return False
+    if device is not None and device != gdevice:
+        raise _reject("gradients on several devices")
+    table, blocks = _grad_table(grads, gdevice)
+    inv = torch.tensor(1.0 / scale, dtype=torch.float32, device=gdevice)
+    _, multiplier, found_inf = ops.grad_stats(table, blocks, inv, max_norm, ops.CLIP_IF_BELOW_ONE)
+    if bool(found_inf.item()):
+        return True
+    owned_ids = {id(p) for p in owned}
+    others = [p.grad for p in parameters if p.grad is not None and id(p) not in owned_ids]
+    if others:
+        other_table, other_blocks = _grad_table(others, gdevice)
+        ops.grad_scale(other_table, other_blocks, multiplier)
+    if device is not None:
+        _run(optimizer, groups, device, multiplier, True)
+    return False
+
+
 class AdamWStepWithFallback:
     """Attempt the fused step when enabled, else (or on failure) ``optimizer.step()``
     (reference adamw.py:27-47)."""

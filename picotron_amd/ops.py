@@ -527,6 +527,46 @@ def clip_grad_norm(table_device: Tensor, total_blocks: int, max_norm: float) -> 
     return out[0], out[1:2]
 
 
+CLIP_CLAMP = 0         # torch.nn.utils.clip_grad_norm_: g *= min(coef, 1)
+CLIP_IF_BELOW_ONE = 1  # the ZeRO optimizer: g *= coef only when coef < 1
+
+
+def grad_stats(
+    table_device: Tensor,
+    total_blocks: int,
+    inv_scale: Tensor | None = None,
+    max_norm: float | None = None,
+    clip_mode: int = CLIP_CLAMP,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(total_norm, grad_scale, found_inf) device scalars over a table's gradients: the
+    norm of g * inv_scale, inv_scale times the clip coefficient (1 without ``max_norm``),
+    and whether any gradient is inf or NaN (int32)."""
+
+    device = _check_cuda(table_device)
+    if inv_scale is not None:
+        _check_cuda(inv_scale)
+        if inv_scale.dtype != torch.float32 or inv_scale.numel() != 1:
+            raise ValueError("inv_scale must be one fp32 element")
+    out = torch.empty(3, dtype=torch.float32, device=device)
+    ws_bytes = _lib.lib().pt_grad_stats_workspace_bytes(int(total_blocks))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
+    _lib.call(
+        "pt_grad_stats",
+        table_device.data_ptr(), table_device.size(0), int(total_blocks), _ptr(inv_scale),
+        -1.0 if max_norm is None else float(max_norm), int(clip_mode), out.data_ptr(),
+        out.data_ptr() + 4, out.data_ptr() + 8, ws.data_ptr(), ws_bytes, _stream(device),
+    )
+    return out[0], out[1:2], out[2:3].view(torch.int32)
+
+
+def grad_scale(table_device: Tensor, total_blocks: int, scale: Tensor) -> None:
+    """g *= scale (fp32 device scalar) in place for every gradient of a table."""
+
+    device = _check_cuda(table_device, scale)
+    _lib.call("pt_grad_scale", table_device.data_ptr(), table_device.size(0), int(total_blocks),
+              scale.data_ptr(), _stream(device))
+
+
 # ------------------------------------------------------------------ utility
 
 

@@ -364,3 +364,33 @@ def test_residual_rmsnorm_oracle_rounds_h_like_torch():
     h, _, _ = o_rms.residual_forward(x, r, torch.ones(32), 1e-6)
     assert h.dtype == torch.bfloat16
     assert torch.equal(h, x + r)  # torch's bf16 add: fp32 sum rounded once
+
+
+def test_zero_unscale_and_check_oracle():
+    g = [torch.tensor([1.5, -3.0, 2.0**-20]), torch.tensor([[7.0, 0.25]])]
+    found, out = o_adamw.unscale_and_check(g, 1024.0)
+    assert not found
+    for a, b in zip(out, g):
+        assert torch.equal(a, b / 1024)  # a power-of-two scale divides exactly
+    bad = [g[0], torch.tensor([1.0, float("nan")])]
+    found, out = o_adamw.unscale_and_check(bad, 1024.0)
+    assert found and all(x is y for x, y in zip(out, bad))  # untouched
+    found, _ = o_adamw.unscale_and_check([torch.tensor([float("-inf")])], 2.0)
+    assert found
+
+
+@pytest.mark.parametrize("max_norm", [0.5, 1e3])
+def test_zero_clip_oracle_matches_torch_clip_when_clipping(max_norm):
+    torch.manual_seed(14)
+    grads = [torch.randn(n, dtype=torch.float64) for n in (10, 100)]
+    total, out = o_adamw.zero_clip_grad_norm(grads, max_norm)
+    params = [torch.nn.Parameter(torch.zeros_like(g)) for g in grads]
+    for p, g in zip(params, grads):
+        p.grad = g.clone()
+    ref_total = torch.nn.utils.clip_grad_norm_(params, max_norm)
+    torch.testing.assert_close(total, ref_total, rtol=1e-12, atol=0)
+    for o, p, g in zip(out, params, grads):
+        if max_norm < 1:  # coefficient below 1: both clip the same way
+            torch.testing.assert_close(o, p.grad, rtol=1e-12, atol=0)
+        else:  # no clipping at all (torch multiplies by exactly 1)
+            assert torch.equal(o, g) and torch.equal(p.grad, g)
