@@ -32,8 +32,8 @@ namespace pt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
-constexpr int64_t kBlockElems = int64_t{kThreads} * 4 * kUnroll;  // 4096 fp32 per block
+constexpr int kUnroll = 1;
+constexpr int64_t kBlockElems = int64_t{kThreads} * 4 * kUnroll;  // 1024 fp32 per block
 
 struct AdamRec {
   int64_t p, g, m, v, n, first_block;

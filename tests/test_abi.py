@@ -51,7 +51,7 @@ def test_workspace_queries():
     assert lib.pt_rmsnorm_bwd_workspace_bytes(3, 128, _lib.PT_FLOAT32) == 2 * 128 * 4
     assert lib.pt_rmsnorm_bwd_workspace_bytes(0, 128, _lib.PT_FLOAT32) == 0
     assert lib.pt_cross_entropy_workspace_bytes(8192) == 16 + 8192 * 4
-    assert lib.pt_adamw_block_elems() == 4096
+    assert lib.pt_adamw_block_elems() == 1024
 
 
 @pytest.mark.parametrize(
@@ -86,3 +86,4 @@ def test_empty_inputs_are_no_ops():
     assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
     assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, 2, None) == _lib.PT_OK
     assert lib.pt_last_error() == b""
+
