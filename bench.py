@@ -661,7 +661,7 @@ class AdamWClipWorkload(AdamWWorkload):
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
         self.out = torch.empty(2, dtype=torch.float32, device="cuda")
         self.bytes_per_step = 36 * n  # norm: read g; step: read p, g, m, v, write p, m, v, g
-        self.dominant = ("fused clip + step (grad_sumsq_kernel + grad_norm_finish_kernel + "
+        self.dominant = ("fused clip + step (grad_stats_kernel + grad_stats_finish_kernel + "
                          "adamw_kernel with the clip coefficient, clipped grads written back)")
         self.dominant_bytes = self.bytes_per_step
         self.description = (

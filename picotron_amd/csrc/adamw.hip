@@ -133,43 +133,72 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
   }
 }
 
-// Per-block statistics of the gradients (table layout as the step; only the g, n and
-// first_block fields are read): the partial sum of squares of u = g * inv_scale (the
+// Statistics of the gradients (table layout as the step; only the g, n and first_block
+// fields are read): per workgroup, the partial sum of squares of u = g * inv_scale (the
 // unscaled gradient, inv_scale = 1 when absent) and, when `nonfinite` is given, whether any
-// g of the block is inf or NaN.
+// g it read is inf or NaN.  A grid of a few workgroups per CU walks the table's blocks,
+// kWalkUnroll at a time (their loads in flight together), so the finish pass adds a few
+// thousand partials; the walk order is fixed by the grid, so the sum is reproducible.
+constexpr int kWalkUnroll = 4;
+
+struct BlockSpan {
+  const float* g;
+  int64_t start, end;
+  bool vec;  // a whole 16-byte-aligned block: one float4 per thread
+};
+
+__device__ __forceinline__ BlockSpan block_span(const AdamRec* __restrict__ table,
+                                                int64_t ntensors, int64_t vb) {
+  const AdamRec r = table[find_tensor(table, ntensors, vb)];
+  BlockSpan b;
+  b.g = reinterpret_cast<const float*>(r.g);
+  b.start = (vb - r.first_block) * kBlockElems;
+  b.end = (b.start + kBlockElems < r.n) ? b.start + kBlockElems : r.n;
+  b.vec = (r.g & 15) == 0 && b.end - b.start == kBlockElems;
+  return b;
+}
+
 __global__ __launch_bounds__(kThreads) void grad_stats_kernel(const AdamRec* __restrict__ table,
-                                                              int64_t ntensors,
+                                                              int64_t ntensors, int64_t nblocks,
                                                               const float* __restrict__ inv_scale,
                                                               float* __restrict__ partial,
                                                               int* __restrict__ nonfinite) {
   __shared__ float red[kThreads / 64];
-  const int64_t blk = blockIdx.x;
-  const AdamRec r = table[find_tensor(table, ntensors, blk)];
-  const int64_t start = (blk - r.first_block) * kBlockElems;
-  const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
-  const float* G = reinterpret_cast<const float*>(r.g);
   const float s = inv_scale != nullptr ? *inv_scale : 1.0f;
   float acc = 0.0f;
   bool bad = false;
-  if ((r.g & 15) == 0 && end - start == kBlockElems) {
-    f32x4 gv[kUnroll];
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWalkUnroll;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWalkUnroll; base < nblocks; base += step) {
+    BlockSpan sp[kWalkUnroll];
+    f32x4 gv[kWalkUnroll];
 #pragma unroll
-    for (int k = 0; k < kUnroll; ++k)
-      gv[k] = __builtin_nontemporal_load(
-          reinterpret_cast<const f32x4*>(G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
-#pragma unroll
-    for (int k = 0; k < kUnroll; ++k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float u = gv[k][j] * s;
-        acc += u * u;
-        bad |= !__builtin_isfinite(gv[k][j]);
+    for (int u = 0; u < kWalkUnroll; ++u) {
+      sp[u].g = nullptr;
+      sp[u].vec = false;
+      sp[u].start = sp[u].end = 0;
+      if (base + u < nblocks) {
+        sp[u] = block_span(table, ntensors, base + u);
+        if (sp[u].vec)
+          gv[u] = __builtin_nontemporal_load(
+              reinterpret_cast<const f32x4*>(sp[u].g + sp[u].start + threadIdx.x * 4));
       }
-  } else {
-    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
-      const float u = G[i] * s;
-      acc += u * u;
-      bad |= !__builtin_isfinite(G[i]);
+    }
+#pragma unroll
+    for (int u = 0; u < kWalkUnroll; ++u) {
+      if (sp[u].vec) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = gv[u][j] * s;
+          acc += x * x;
+          bad |= !__builtin_isfinite(gv[u][j]);
+        }
+      } else {
+        for (int64_t i = sp[u].start + threadIdx.x; i < sp[u].end; i += kThreads) {
+          const float x = sp[u].g[i] * s;
+          acc += x * x;
+          bad |= !__builtin_isfinite(sp[u].g[i]);
+        }
+      }
     }
   }
   acc = wave_sum(acc);
@@ -180,9 +209,16 @@ __global__ __launch_bounds__(kThreads) void grad_stats_kernel(const AdamRec* __r
     float t = 0.0f;
 #pragma unroll
     for (int w = 0; w < kThreads / 64; ++w) t += red[w];
-    partial[blk] = t;
-    if (nonfinite != nullptr) nonfinite[blk] = any_bad;
+    partial[blockIdx.x] = t;
+    if (nonfinite != nullptr) nonfinite[blockIdx.x] = any_bad;
   }
+}
+
+// Number of workgroups of the statistics and scaling walks.
+int walk_grid(int64_t nblocks) {
+  const int64_t want = (nblocks + kWalkUnroll - 1) / kWalkUnroll;
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 32;
+  return static_cast<int>(want < cap ? (want < 1 ? 1 : want) : cap);
 }
 
 // total_norm = sqrt(sum of the partials, added in double in a fixed order), the gradient
@@ -227,33 +263,38 @@ __global__ __launch_bounds__(1024) void grad_stats_finish_kernel(
 }
 
 // In-place g *= *scale over every gradient of the table; nothing at all when the scale is
-// exactly 1 (a clip that does not clip).  A grid of a few blocks per CU walks the table's
-// blocks, so that case costs one small launch.
+// exactly 1 (a clip that does not clip).  Walks the table like grad_stats_kernel.
 __global__ __launch_bounds__(kThreads) void grad_scale_kernel(const AdamRec* __restrict__ table,
                                                               int64_t ntensors, int64_t nblocks,
                                                               const float* __restrict__ scale) {
   const float s = *scale;
   if (s == 1.0f) return;
-  for (int64_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
-    const AdamRec r = table[find_tensor(table, ntensors, blk)];
-    const int64_t start = (blk - r.first_block) * kBlockElems;
-    const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
-    float* G = reinterpret_cast<float*>(r.g);
-    if ((r.g & 15) == 0 && end - start == kBlockElems) {
-      f32x4 gv[kUnroll];
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWalkUnroll;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWalkUnroll; base < nblocks; base += step) {
+    BlockSpan sp[kWalkUnroll];
+    f32x4 gv[kWalkUnroll];
 #pragma unroll
-      for (int k = 0; k < kUnroll; ++k)
-        gv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
-            G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) gv[k][j] = gv[k][j] * s;
-        __builtin_nontemporal_store(gv[k], reinterpret_cast<f32x4*>(
-            G + start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4));
+    for (int u = 0; u < kWalkUnroll; ++u) {
+      sp[u].g = nullptr;
+      sp[u].vec = false;
+      sp[u].start = sp[u].end = 0;
+      if (base + u < nblocks) {
+        sp[u] = block_span(table, ntensors, base + u);
+        if (sp[u].vec)
+          gv[u] = __builtin_nontemporal_load(
+              reinterpret_cast<const f32x4*>(sp[u].g + sp[u].start + threadIdx.x * 4));
       }
-    } else {
-      for (int64_t i = start + threadIdx.x; i < end; i += kThreads) G[i] = G[i] * s;
+    }
+#pragma unroll
+    for (int u = 0; u < kWalkUnroll; ++u) {
+      float* G = const_cast<float*>(sp[u].g);
+      if (sp[u].vec) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gv[u][j] = gv[u][j] * s;
+        __builtin_nontemporal_store(gv[u], reinterpret_cast<f32x4*>(G + sp[u].start + threadIdx.x * 4));
+      } else {
+        for (int64_t i = sp[u].start + threadIdx.x; i < sp[u].end; i += kThreads) G[i] = G[i] * s;
+      }
     }
   }
 }
@@ -326,12 +367,17 @@ int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_
   return check_launch("pt_adamw_step_scaled");
 }
 
+// One fp32 partial (and one int flag) per workgroup of the statistics walk, which has at
+// most ceil(total_blocks / kWalkUnroll) workgroups.
 size_t pt_clip_grad_norm_workspace_bytes(int64_t total_blocks) {
-  return total_blocks < 0 ? 0 : static_cast<size_t>(total_blocks) * sizeof(float);
+  if (total_blocks < 0) return 0;
+  return static_cast<size_t>((total_blocks + kWalkUnroll - 1) / kWalkUnroll) * sizeof(float);
 }
 
 size_t pt_grad_stats_workspace_bytes(int64_t total_blocks) {
-  return total_blocks < 0 ? 0 : static_cast<size_t>(total_blocks) * (sizeof(float) + sizeof(int));
+  if (total_blocks < 0) return 0;
+  const size_t parts = static_cast<size_t>((total_blocks + kWalkUnroll - 1) / kWalkUnroll);
+  return (parts * sizeof(float) + 15) / 16 * 16 + parts * sizeof(int);
 }
 
 }  // extern "C"
@@ -345,16 +391,17 @@ int grad_stats_run(const char* fn, const int64_t* table, int64_t n_tensors, int6
                    hipStream_t st) {
   int rc = check_table(fn, table, n_tensors, total_blocks);
   if (rc != -1 && rc != PT_OK) return rc;
+  int64_t nparts = 0;  // no gradients: the norm of nothing is 0
   if (rc == PT_OK) {
-    hipLaunchKernelGGL(grad_stats_kernel, dim3(static_cast<unsigned>(total_blocks)),
-                       dim3(kThreads), 0, st, reinterpret_cast<const AdamRec*>(table), n_tensors,
-                       inv_scale, partial, nonfinite);
+    const int grid = walk_grid(total_blocks);
+    hipLaunchKernelGGL(grad_stats_kernel, dim3(grid), dim3(kThreads), 0, st,
+                       reinterpret_cast<const AdamRec*>(table), n_tensors, total_blocks, inv_scale,
+                       partial, nonfinite);
     if (int lrc = check_launch(fn)) return lrc;
-  } else {
-    total_blocks = 0;  // no gradients: the norm of nothing is 0
+    nparts = grid;
   }
   hipLaunchKernelGGL(grad_stats_finish_kernel, dim3(1), dim3(1024), 0, st, partial, nonfinite,
-                     total_blocks, static_cast<float>(max_norm), clip_mode, inv_scale, total_out,
+                     nparts, static_cast<float>(max_norm), clip_mode, inv_scale, total_out,
                      scale_out, found_out);
   return check_launch(fn);
 }
@@ -391,7 +438,11 @@ int pt_grad_stats(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
        !aligned16(workspace)))
     return fail(PT_EINVAL, "pt_grad_stats: workspace too small or not 16-byte aligned");
   float* partial = static_cast<float*>(workspace);
-  int* nonfinite = partial != nullptr ? reinterpret_cast<int*>(partial + total_blocks) : nullptr;
+  const int64_t parts = (total_blocks + kWalkUnroll - 1) / kWalkUnroll;
+  int* nonfinite = partial != nullptr
+                       ? reinterpret_cast<int*>(reinterpret_cast<char*>(partial) +
+                                                (parts * sizeof(float) + 15) / 16 * 16)
+                       : nullptr;
   return grad_stats_run("pt_grad_stats", table, n_tensors, total_blocks, inv_scale, max_norm,
                         clip_mode, total_norm_out, grad_scale_out, found_inf_out, partial,
                         nonfinite, as_stream(stream));
@@ -403,10 +454,9 @@ int pt_grad_scale(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
   if (rc == -1) return ok();
   if (rc != PT_OK) return rc;
   if (!scale) return fail(PT_EINVAL, "pt_grad_scale: null scale");
-  const int64_t cap = static_cast<int64_t>(num_cus()) * 16;
-  const unsigned grid = static_cast<unsigned>(total_blocks < cap ? total_blocks : cap);
-  hipLaunchKernelGGL(grad_scale_kernel, dim3(grid), dim3(kThreads), 0, as_stream(stream),
-                     reinterpret_cast<const AdamRec*>(table), n_tensors, total_blocks, scale);
+  hipLaunchKernelGGL(grad_scale_kernel, dim3(walk_grid(total_blocks)), dim3(kThreads), 0,
+                     as_stream(stream), reinterpret_cast<const AdamRec*>(table), n_tensors,
+                     total_blocks, scale);
   return check_launch("pt_grad_scale");
 }
 
