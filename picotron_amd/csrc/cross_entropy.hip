@@ -10,11 +10,12 @@
 //   1. ce_prepare: one block counts the non-ignored targets (n_valid) into the workspace
 //      and clears the status word.
 //   2. ce_rows: one 1024-thread workgroup per row.  The row is loaded once into registers
-//      (VPT 16-byte vectors per thread) and reduced to its max; exp(x - max) is then
-//      computed once per element, summed in fp32 and kept in the registers in place of the
-//      logit, so the gradient softmax / n_valid is written from registers without a second
-//      exponential: HBM sees one read and one write of the logits.  The target element's
-//      gradient (softmax_t - 1) / n_valid is computed from the exact fp32 target logit.
+//      (VPT 16-byte vectors per thread, raw buffer loads whose hardware range check drops
+//      the ragged end) and reduced by an online max / sum of exp(x - max) as the vectors
+//      arrive; each exp is kept in the registers in place of its logit, so the gradient
+//      softmax / n_valid is written from registers with one multiply per element and no
+//      second exponential: HBM sees one read and one write of the logits.  The target
+//      element's gradient (softmax_t - 1) / n_valid comes from the exact fp32 target logit.
 //      Rows too long for registers, or not 16-byte aligned, use ce_rows_stream (online
 //      max / sum, then a second read).  Each row's fp32 loss goes to the workspace.
 //   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
@@ -45,6 +46,8 @@ constexpr size_t kHeader = 16;
 __device__ __forceinline__ float* row_losses(CeWork* ws) {
   return reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kHeader);
 }
+
+__device__ __forceinline__ float inv_n_of(const CeWork* ws) { return 1.0f / ws->n_valid; }
 
 __device__ __forceinline__ float exp2_(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -150,76 +153,194 @@ __device__ __forceinline__ float target_grad(float mx, float se, float xt, float
   return (exp_shifted(xt, mx) / se - 1.0f) * inv_n;
 }
 
-// exp(x - max) is kept in the storage type in place of the logit.  fp16 holds it scaled by
-// 2^15 (at most 32768 < 65504), so that values down to 2^-29 keep full fp16 precision
-// instead of going subnormal; fp32 and bf16 have fp32's exponent range and need no scale.
+// Where a row lives and what its target is; uniform across the block.  A row without a
+// target (ignore_index, or a position i >= valid_inner) has skip set.
+struct RowRef {
+  int64_t off;
+  int64_t tgt;
+  bool skip;
+};
+
+__device__ __forceinline__ RowRef row_ref(int64_t row, int64_t inner, int64_t valid_inner,
+                                          int64_t os, int64_t is,
+                                          const int64_t* __restrict__ targets, int64_t tos,
+                                          int64_t tis, int64_t ignore_index) {
+  const int64_t o = row / inner, ii = row - o * inner;
+  RowRef r;
+  r.off = o * os + ii * is;
+  r.tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
+  r.skip = r.tgt == ignore_index;
+  return r;
+}
+
+// Raw buffer resource (stride 0) over `bytes` bytes at `base`: the hardware drops loads
+// past the end (they return 0) and stores past the end, so a row's ragged last vectors need
+// no branches, and a resource of 0 bytes turns a row's loads into no-ops without memory
+// traffic.  The range check covers the VGPR offset plus the instruction's immediate offset
+// but not the SGPR offset, so every access below puts its whole offset in the VGPR operand
+// and passes an SGPR offset of 0.  kBufferWord3 is the gfx9-family data-format word for
+// untyped 32-bit access.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kNonTemporal = 2;  // buffer cache policy bit: no reuse expected
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kBufferWord3);
+}
+
+// exp(x - m) kept in the storage type in place of the logit: fp16 holds it scaled by 2^15
+// (at most 32768 < 65504), so that values down to 2^-29 keep full fp16 precision instead of
+// going subnormal; fp32 and bf16 have fp32's exponent range and need no scale.
 template <typename T>
 constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
 
+// The bit pattern of two / one -inf in the storage type, for masking vectors past the row.
+template <typename T>
+constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000u
+                                 : std::is_same<T, _Float16>::value ? 0xfc00fc00u
+                                                                    : 0xff80ff80u;
+
+// Register-resident rows, VPT 16-byte vectors per thread, one 1024-thread workgroup per row
+// (a CU holds one such workgroup; when it retires its stores drain while the next row's
+// workgroup loads, which keeps reads and writes in flight together).  Per row:
+//   1. an online max / sum per thread as the vectors arrive: chunk k's elements become
+//      e = exp(x - m_k), m_k the thread's running max after the chunk, summed in fp32 and
+//      kept in the storage type in place of the logits; then the max and the rescaled sums
+//      are reduced across the wave by shuffles and across the block through LDS (one
+//      barrier);
+//   2. the gradient e * exp(m_k - M) / (S * n_valid), one multiply per element with a factor
+//      per chunk.  The thread holding the target writes the row loss and, after its own
+//      vector store of that address, the target element (softmax_t - 1) / n_valid.
+// Keeping e rounds the softmax twice in 16-bit storage (once as e, once as the gradient),
+// a relative error of at most 2 units of the storage type's last place.
+// The launch guarantees VPT is the smallest of 1, 2, 4, 8, 16 that covers the row, so the
+// vectors of chunks k < VPT / 2 are always inside it.
 template <typename T, int VPT>
 __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
     int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
     int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
-  __shared__ float red[kWaves];
-  __shared__ float s_target_logit;
-  T* p = nullptr;
-  int tgt = 0;
-  if (!ce_row_begin<T, V, true>(logits, inner, valid_inner, os, is, vocab, targets, tos, tis,
-                                ignore_index, write_grad, ws, &p, &tgt, &s_target_logit))
+  constexpr int kChunkBytes = kThreads * 16;
+  __shared__ float red_m[kWaves];
+  __shared__ float red_s[kWaves];
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64;
+  const int64_t row = blockIdx.x;
+  const int row_bytes = vocab * static_cast<int>(sizeof(T));
+  const int voff = tid * 16;
+  const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
+  const auto buf = row_buffer(logits + cur.off, row_bytes);
+
+  if (cur.skip) {
+    if (write_grad) {
+#pragma unroll
+      for (int k = 0; k < VPT; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf,
+                                               voff + k * kChunkBytes, 0, kNonTemporal);
+    }
+    if (tid == 0) row_losses(ws)[row] = 0.0f;
     return;
+  }
 
   Vec16<T> v[VPT];
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int e = (threadIdx.x + k * kThreads) * V;
-    if (e < vocab) v[k].raw = load16<true>(p + e);
-  }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int e = (threadIdx.x + k * kThreads) * V;
-    if (e < vocab) {
-#pragma unroll
-      for (int i = 0; i < V; ++i) mx = fmaxf(mx, Elem<T>::to_f32(v[k].e[i]));
-    }
-  }
-  mx = block_reduce_max(mx, red);
-  float se = 0.0f;
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int e = (threadIdx.x + k * kThreads) * V;
-    if (e < vocab) {
-#pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const float ex = exp_shifted(Elem<T>::to_f32(v[k].e[i]), mx);
-        se += ex;
-        v[k].e[i] = Elem<T>::from_f32(ex * kExpScale<T>);
-      }
-    }
-  }
-  se = block_reduce_sum(se, red);
-  const float xt = s_target_logit;
-  if (threadIdx.x == 0) row_losses(ws)[blockIdx.x] = row_loss(mx, se, xt);
-  if (!write_grad) return;
+  for (int k = 0; k < VPT; ++k)
+    v[k].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, voff + k * kChunkBytes, 0, kNonTemporal);
 
-  const float inv_n = 1.0f / ws->n_valid;
-  const float scale = (inv_n / se) * (1.0f / kExpScale<T>);
-  const float gt = target_grad(mx, se, xt, inv_n);
+  // The target's vector index, its owner thread, chunk and lane are uniform; the owner
+  // picks the exact target logit out of its registers.  A target outside [0, vocab) sets
+  // status bit 0 and gives the row a NaN loss, as no logit is its own.
+  const bool bad = cur.tgt < 0 || cur.tgt >= vocab;
+  const int tvec = bad ? 0 : static_cast<int>(cur.tgt / V);
+  const int owner = bad ? 0 : tvec % kThreads;
+  const int tk = tvec / kThreads, ti = bad ? 0 : static_cast<int>(cur.tgt % V);
+  if (bad && tid == 0) atomicOr(&ws->status, 1);
+  float xt = NAN;
+  if (!bad && tid == owner) {
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int e = (threadIdx.x + k * kThreads) * V;
-    if (e < vocab) {
-      float g[V];
-#pragma unroll
-      for (int i = 0; i < V; ++i) g[i] = Elem<T>::to_f32(v[k].e[i]) * scale;
-      if (static_cast<unsigned>(tgt - e) < static_cast<unsigned>(V)) {
+    for (int k = 0; k < VPT; ++k) {
+      if (k == tk) {
 #pragma unroll
         for (int i = 0; i < V; ++i)
-          if (e + i == tgt) g[i] = gt;
+          if (i == ti) xt = Elem<T>::to_f32(v[k].e[i]);
       }
-      store_f32<T, true, true>(p + e, g, V);
+    }
+  }
+
+  float m = -INFINITY, s = 0.0f;
+  float mk[VPT];  // running max after chunk k: the reference of the exps kept for chunk k
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    Vec16<T> r = v[k];
+    if (k >= VPT / 2 && (tid + k * kThreads) * V >= vocab) {
+      const uint32_t ninf = kNegInfWord<T>;
+      r.raw = u32x4{ninf, ninf, ninf, ninf};
+    }
+    float x[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
+    float cm = x[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
+    const float nm = fmaxf(m, cm);
+    const float ref = nm == -INFINITY ? 0.0f : nm;
+    float add = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float e = exp_shifted(x[i], ref);
+      add += e;
+      v[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+    }
+    // Packed here: left to itself the optimiser would carry the fp32 exps across the
+    // barrier into the gradient branch, twice the registers.
+    asm volatile("" : "+v"(v[k].raw));
+    s = s * exp_shifted(m, ref) + add;
+    m = nm;
+    mk[k] = nm;
+  }
+  // Max first, then one rescale per partial sum (a max of -inf is shifted by 0, as above).
+  const float mw = wave_max(m);
+  const float sw = wave_sum(s * exp_shifted(m, mw == -INFINITY ? 0.0f : mw));
+  if (lane == 0) {
+    red_m[wave] = mw;
+    red_s[wave] = sw;
+  }
+  __syncthreads();
+  float M = red_m[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, red_m[w]);
+  const float refM = M == -INFINITY ? 0.0f : M;
+  float S = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) S += red_s[w] * exp_shifted(red_m[w], refM);
+  if (tid == owner) row_losses(ws)[row] = row_loss(M, S, xt);
+  if (!write_grad) return;
+
+  const float scale = inv_n_of(ws) / S;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    Vec16<T> out;
+    // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf (it held only
+    // -inf logits, whose exps are 0).
+    const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(v[k].e[i]) * f);
+    }
+    // One add per store rather than sixteen offsets held in registers across the row.
+    int vo = voff + k * kChunkBytes;
+    asm volatile("" : "+v"(vo));
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, vo, 0, kNonTemporal);
+  }
+  if (!bad && tid == owner) {
+    Vec16<T> one;
+    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n_of(ws)));
+    const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
+    if constexpr (sizeof(T) == 4) {
+      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
+                                            buf, toff, 0, kNonTemporal);
     }
   }
 }
