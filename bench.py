@@ -875,6 +875,9 @@ def main() -> int:
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="rmsnorm")
     parser.add_argument("--layers", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extra", action="store_true",
+                        help="skip the workload's comparison measurements (e.g. the unfused "
+                             "sequence), so that a profile holds only the timed launches")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -945,7 +948,7 @@ def main() -> int:
     if traffic:
         roofline["traffic_source"] = traffic.get("source")
 
-    extra = wl.extra(args.steps)
+    extra = None if args.no_extra else wl.extra(args.steps)
 
     cpu = None
     if not args.no_cpu_baseline:
