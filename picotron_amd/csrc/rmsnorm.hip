@@ -28,6 +28,9 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __r
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) s += v[u];
     }
+    // The remainder (fewer than kUnroll partials per group) in batches of 16 independent
+    // loads, so that it costs a few round trips rather than one per partial.
+#pragma unroll 16
     for (; i < nparts; i += kGroups) s += p[i * cols];
   }
   lds[grp][col] = s;

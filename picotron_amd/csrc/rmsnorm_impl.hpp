@@ -478,16 +478,29 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
       ra += 3 * group_stride;
     }
   } else if constexpr (PREFETCH == 1) {
+    // The loop body issues its two prefetches unconditionally (both rows are within the
+    // block's iterations), so the wait for the row being reduced counts only that row's
+    // loads: a prefetch under a branch would make the compiler wait for everything at the
+    // join.  The last one or two rows are peeled.
     Buf a, b;
     load(a, ra);
-    for (int it = 0; it < iters; it += 2) {
+    int it = 0;
+    for (; it + 2 < iters; it += 2) {
       const int64_t rb = ra + group_stride;
-      if (it + 1 < iters) load(b, rb);
+      load(b, rb);
       process(a, ra, 0);
       const int64_t rc = rb + group_stride;
-      if (it + 2 < iters) load(a, rc);
-      if (it + 1 < iters) process(b, rb, 1);
+      load(a, rc);
+      process(b, rb, 1);
       ra = rc;
+    }
+    if (it + 1 < iters) {
+      const int64_t rb = ra + group_stride;
+      load(b, rb);
+      process(a, ra, 0);
+      process(b, rb, 1);
+    } else {
+      process(a, ra, 0);
     }
   } else {
     for (int it = 0; it < iters; ++it) {
