@@ -152,17 +152,43 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float v
 
 // ------------------------------------------------------------------ reductions
 
-// Butterfly sum over the 64 lanes of a wave; every lane receives the total.
+// Wave reductions on DPP lane moves (register-to-register, a few cycles each) instead of
+// LDS permutes: two quad swaps, a half-row and a row mirror leave every lane of each
+// 16-lane row holding that row's result (bitwise equal in all of its lanes, since each
+// step combines the same two values in either order); the four row results are then read
+// into scalars and combined in row order, so every lane receives the same total.  All 64
+// lanes must be active.
+namespace dpp {
+constexpr int kQuadSwap1 = 0xb1;     // quad_perm [1, 0, 3, 2]
+constexpr int kQuadSwap2 = 0x4e;     // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+}  // namespace dpp
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m);
-  return v;
+  v += dpp::move<dpp::kQuadSwap1>(v);
+  v += dpp::move<dpp::kQuadSwap2>(v);
+  v += dpp::move<dpp::kRowHalfMirror>(v);
+  v += dpp::move<dpp::kRowMirror>(v);
+  return ((dpp::lane(v, 0) + dpp::lane(v, 16)) + dpp::lane(v, 32)) + dpp::lane(v, 48);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-  return v;
+  v = fmaxf(v, dpp::move<dpp::kQuadSwap1>(v));
+  v = fmaxf(v, dpp::move<dpp::kQuadSwap2>(v));
+  v = fmaxf(v, dpp::move<dpp::kRowHalfMirror>(v));
+  v = fmaxf(v, dpp::move<dpp::kRowMirror>(v));
+  return fmaxf(fmaxf(dpp::lane(v, 0), dpp::lane(v, 16)), fmaxf(dpp::lane(v, 32), dpp::lane(v, 48)));
 }
 
 constexpr int kWave = 64;
