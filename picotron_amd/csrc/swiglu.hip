@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_elem_kernel(const T* __restric
 }
 
 constexpr int kFwdUnroll = 4;
-constexpr int kBwdUnroll = 2;
+constexpr int kBwdUnroll = 4;
 // Streams above this many bytes bypass cache retention (nontemporal).
 constexpr int64_t kNontemporalBytes = int64_t{64} << 20;
 

@@ -18,7 +18,7 @@ def close_fp32(
     """|a - e| <= rtol*|e| + 1e-6*scale.  ``scale`` defaults to max|e|; pass the magnitude of
     the summands when the result is a near-cancelling difference of them."""
 
-    expected = expected.to(actual.device)
+    expected = expected.detach().to(actual.device)
     if scale is None:
         scale = float(expected.abs().max()) if expected.numel() else 0.0
     torch.testing.assert_close(
@@ -29,7 +29,7 @@ def close_fp32(
 def close(
     actual: torch.Tensor, expected: torch.Tensor, dtype: torch.dtype, scale: float | None = None
 ) -> None:
-    expected = expected.to(actual.device)
+    expected = expected.detach().to(actual.device)
     if dtype == torch.float32:
         close_fp32(actual, expected, scale=scale)
     elif dtype == torch.bfloat16:
