@@ -39,20 +39,23 @@ struct RopeTensor {
   int64_t blocks;  // blocks assigned to this tensor
 };
 
-template <typename T, int LAYOUT, bool ALIGNED>
-__device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int head_dim,
+// Item, row and the three row indices fit in 32 bits (pt_rope bounds items by 2^32), so
+// they are decoded with 32-bit divisions; only the memory offsets are 64-bit.
+template <typename T, int LAYOUT, bool ALIGNED, bool NT>
+__device__ __forceinline__ void rope_item(const RopeTensor& t, uint32_t item, int head_dim,
                                           const float* __restrict__ cos_t,
                                           const float* __restrict__ sin_t, float sign) {
   constexpr int V = ALIGNED ? Elem<T>::VEC : 2;
   const int half = head_dim / 2;
-  const int per_row = items_per_row<T, LAYOUT, ALIGNED>(head_dim);
-  const int64_t row = item / per_row;
+  const uint32_t per_row = static_cast<uint32_t>(items_per_row<T, LAYOUT, ALIGNED>(head_dim));
+  const uint32_t row = item / per_row;
   const int j = static_cast<int>(item - row * per_row);
+  const uint32_t n2 = static_cast<uint32_t>(t.n[2]), n1 = static_cast<uint32_t>(t.n[1]);
   int64_t idx[3];
-  idx[2] = row % t.n[2];
-  const int64_t r1 = row / t.n[2];
-  idx[1] = r1 % t.n[1];
-  idx[0] = r1 / t.n[1];
+  const uint32_t r1 = row / n2;
+  idx[2] = row - r1 * n2;
+  idx[0] = r1 / n1;
+  idx[1] = r1 - static_cast<uint32_t>(idx[0]) * n1;
   const int64_t xo = idx[0] * t.xs[0] + idx[1] * t.xs[1] + idx[2] * t.xs[2];
   const int64_t yo = idx[0] * t.ys[0] + idx[1] * t.ys[1] + idx[2] * t.ys[2];
   const int64_t s = idx[t.seq_dim];
@@ -65,7 +68,7 @@ __device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int
     // elements [j*V, j*V + V) = pairs [j*V/2, j*V/2 + V/2)
     float a[V];
     if constexpr (ALIGNED) {
-      load_f32<T, true>(xr + j * V, a, V);
+      load_f32<T, true, NT>(xr + j * V, a, V);
     } else {
       a[0] = Elem<T>::to_f32(xr[2 * j]);
       a[1] = Elem<T>::to_f32(xr[2 * j + 1]);
@@ -81,7 +84,7 @@ __device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int
       o[2 * p + 1] = e * sn + od * c;
     }
     if constexpr (ALIGNED) {
-      store_f32<T, true>(yr + j * V, o, V);
+      store_f32<T, true, NT>(yr + j * V, o, V);
     } else {
       yr[2 * j] = Elem<T>::from_f32(o[0]);
       yr[2 * j + 1] = Elem<T>::from_f32(o[1]);
@@ -90,8 +93,8 @@ __device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int
     constexpr int P = ALIGNED ? Elem<T>::VEC : 1;  // pairs per item
     float a[P], b[P];
     if constexpr (ALIGNED) {
-      load_f32<T, true>(xr + j * P, a, P);
-      load_f32<T, true>(xr + half + j * P, b, P);
+      load_f32<T, true, NT>(xr + j * P, a, P);
+      load_f32<T, true, NT>(xr + half + j * P, b, P);
     } else {
       a[0] = Elem<T>::to_f32(xr[j]);
       b[0] = Elem<T>::to_f32(xr[half + j]);
@@ -106,8 +109,8 @@ __device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int
       ob[p] = a[p] * sn + b[p] * c;
     }
     if constexpr (ALIGNED) {
-      store_f32<T, true>(yr + j * P, oa, P);
-      store_f32<T, true>(yr + half + j * P, ob, P);
+      store_f32<T, true, NT>(yr + j * P, oa, P);
+      store_f32<T, true, NT>(yr + half + j * P, ob, P);
     } else {
       yr[j] = Elem<T>::from_f32(oa[0]);
       yr[half + j] = Elem<T>::from_f32(ob[0]);
@@ -115,19 +118,19 @@ __device__ __forceinline__ void rope_item(const RopeTensor& t, int64_t item, int
   }
 }
 
-template <typename T, int LAYOUT, bool ALIGNED>
+template <typename T, int LAYOUT, bool ALIGNED, bool NT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t0, RopeTensor t1, int head_dim,
                                                    const float* __restrict__ cos_t,
                                                    const float* __restrict__ sin_t, float sign) {
-  int64_t b = blockIdx.x;
+  uint32_t b = blockIdx.x;
   const RopeTensor* t = &t0;
   if (b >= t0.blocks) {
-    b -= t0.blocks;
+    b -= static_cast<uint32_t>(t0.blocks);
     t = &t1;
   }
-  const int64_t item = b * 256 + threadIdx.x;
+  const uint32_t item = b * 256u + threadIdx.x;
   if (item >= t->items) return;
-  rope_item<T, LAYOUT, ALIGNED>(*t, item, head_dim, cos_t, sin_t, sign);
+  rope_item<T, LAYOUT, ALIGNED, NT>(*t, item, head_dim, cos_t, sin_t, sign);
 }
 
 bool parse(const void* x, void* y, const int64_t* d, int64_t head_dim, int64_t table_rows,
@@ -176,6 +179,8 @@ bool parse(const void* x, void* y, const int64_t* d, int64_t head_dim, int64_t t
   return true;
 }
 
+constexpr int64_t kNontemporalBytes = int64_t{64} << 20;
+
 template <typename T, int LAYOUT, bool ALIGNED>
 void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const float* s,
             float sign, hipStream_t st) {
@@ -187,9 +192,16 @@ void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const 
   const int64_t blocks = t0.blocks + t1.blocks;
   if (blocks == 0) return;
   // pt_rope has checked that (rows0 + rows1) * head_dim / 2 + 512 < 2^32, which bounds
-  // blocks * 256 for every layout.
-  hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+  // blocks * 256 for every layout.  Streams larger than the caches are touched once:
+  // nontemporal loads and stores.
+  const int64_t bytes = (t0.rows + t1.rows) * head_dim * static_cast<int64_t>(sizeof(T));
+  if (bytes > kNontemporalBytes) {
+    hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+  } else {
+    hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED, false>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+  }
 }
 
 template <typename T>
