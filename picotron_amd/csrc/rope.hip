@@ -39,84 +39,124 @@ struct RopeTensor {
   int64_t blocks;  // blocks assigned to this tensor
 };
 
-// Item, row and the three row indices fit in 32 bits (pt_rope bounds items by 2^32), so
-// they are decoded with 32-bit divisions; only the memory offsets are 64-bit.
+// One work item in two phases, so that a thread can have several items' loads in flight
+// before it computes and stores any of them (the output may alias the input, so the
+// compiler would not move a later item's loads above an earlier item's stores).  The pair
+// members are held as a[p] (first) and b[p] (second): interleaved rows pair elements
+// (2i, 2i+1) of one vector, rotate-half rows pair element i of the first half with element
+// i of the second.  Item, row and the three row indices fit in 32 bits (pt_rope bounds
+// items by 2^32), so they are decoded with 32-bit divisions; only memory offsets are 64-bit.
 template <typename T, int LAYOUT, bool ALIGNED, bool NT>
-__device__ __forceinline__ void rope_item(const RopeTensor& t, uint32_t item, int head_dim,
-                                          const float* __restrict__ cos_t,
-                                          const float* __restrict__ sin_t, float sign) {
-  constexpr int V = ALIGNED ? Elem<T>::VEC : 2;
-  const int half = head_dim / 2;
-  const uint32_t per_row = static_cast<uint32_t>(items_per_row<T, LAYOUT, ALIGNED>(head_dim));
-  const uint32_t row = item / per_row;
-  const int j = static_cast<int>(item - row * per_row);
-  const uint32_t n2 = static_cast<uint32_t>(t.n[2]), n1 = static_cast<uint32_t>(t.n[1]);
-  int64_t idx[3];
-  const uint32_t r1 = row / n2;
-  idx[2] = row - r1 * n2;
-  idx[0] = r1 / n1;
-  idx[1] = r1 - static_cast<uint32_t>(idx[0]) * n1;
-  const int64_t xo = idx[0] * t.xs[0] + idx[1] * t.xs[1] + idx[2] * t.xs[2];
-  const int64_t yo = idx[0] * t.ys[0] + idx[1] * t.ys[1] + idx[2] * t.ys[2];
-  const int64_t s = idx[t.seq_dim];
-  const T* xr = static_cast<const T*>(t.x) + xo;
-  T* yr = static_cast<T*>(t.y) + yo;
-  const float* cr = cos_t + s * half;
-  const float* sr = sin_t + s * half;
+struct RopeWork {
+  static constexpr int V = ALIGNED ? Elem<T>::VEC : 2;
+  static constexpr int P = LAYOUT == 0 ? V / 2 : (ALIGNED ? Elem<T>::VEC : 1);  // pairs
+  // Raw storage until store(): converting in load() would wait for the data there.
+  Vec16<T> va, vb;  // aligned: interleaved vector (va) or the two half vectors (va, vb)
+  T ea[2], eb[2];   // element path: interleaved (ea[0], ea[1]) or rotate-half (ea[0], eb[0])
+  float c[P], s[P];
+  T* ya;  // first members (interleaved: the whole vector)
+  T* yb;  // second members (rotate-half)
 
-  if constexpr (LAYOUT == 0) {
-    // elements [j*V, j*V + V) = pairs [j*V/2, j*V/2 + V/2)
-    float a[V];
-    if constexpr (ALIGNED) {
-      load_f32<T, true, NT>(xr + j * V, a, V);
+  __device__ __forceinline__ void load(const RopeTensor& t, uint32_t item, int head_dim,
+                                       const float* __restrict__ cos_t,
+                                       const float* __restrict__ sin_t) {
+    const int half = head_dim / 2;
+    const uint32_t per_row = static_cast<uint32_t>(items_per_row<T, LAYOUT, ALIGNED>(head_dim));
+    const uint32_t row = item / per_row;
+    const int j = static_cast<int>(item - row * per_row);
+    const uint32_t n2 = static_cast<uint32_t>(t.n[2]), n1 = static_cast<uint32_t>(t.n[1]);
+    int64_t idx[3];
+    const uint32_t r1 = row / n2;
+    idx[2] = row - r1 * n2;
+    idx[0] = r1 / n1;
+    idx[1] = r1 - static_cast<uint32_t>(idx[0]) * n1;
+    const int64_t xo = idx[0] * t.xs[0] + idx[1] * t.xs[1] + idx[2] * t.xs[2];
+    const int64_t yo = idx[0] * t.ys[0] + idx[1] * t.ys[1] + idx[2] * t.ys[2];
+    const int64_t pos = idx[t.seq_dim];
+    const T* xr = static_cast<const T*>(t.x) + xo;
+    T* yr = static_cast<T*>(t.y) + yo;
+    const int i0 = j * P;  // first pair of the item
+    if constexpr (LAYOUT == 0) {
+      if constexpr (ALIGNED) {
+        va.raw = load16<NT>(xr + j * V);
+      } else {
+        ea[0] = xr[2 * j];
+        ea[1] = xr[2 * j + 1];
+      }
+      ya = yr + j * V;
+      yb = ya;
     } else {
-      a[0] = Elem<T>::to_f32(xr[2 * j]);
-      a[1] = Elem<T>::to_f32(xr[2 * j + 1]);
+      if constexpr (ALIGNED) {
+        va.raw = load16<NT>(xr + i0);
+        vb.raw = load16<NT>(xr + half + i0);
+      } else {
+        ea[0] = xr[j];
+        eb[0] = xr[half + j];
+      }
+      ya = yr + i0;
+      yb = yr + half + i0;
     }
-    float o[V];
+    const float* cr = cos_t + pos * half + i0;
+    const float* sr = sin_t + pos * half + i0;
 #pragma unroll
-    for (int p = 0; p < V / 2; ++p) {
-      const int i = j * (V / 2) + p;
-      const float c = cr[i];
-      const float sn = sign * sr[i];
-      const float e = a[2 * p], od = a[2 * p + 1];
-      o[2 * p] = e * c - od * sn;
-      o[2 * p + 1] = e * sn + od * c;
+    for (int p = 0; p < P; ++p) {
+      c[p] = cr[p];
+      s[p] = sr[p];
     }
-    if constexpr (ALIGNED) {
-      store_f32<T, true, NT>(yr + j * V, o, V);
-    } else {
-      yr[2 * j] = Elem<T>::from_f32(o[0]);
-      yr[2 * j + 1] = Elem<T>::from_f32(o[1]);
-    }
-  } else {
-    constexpr int P = ALIGNED ? Elem<T>::VEC : 1;  // pairs per item
+  }
+
+  __device__ __forceinline__ void store(float sign) const {
     float a[P], b[P];
-    if constexpr (ALIGNED) {
-      load_f32<T, true, NT>(xr + j * P, a, P);
-      load_f32<T, true, NT>(xr + half + j * P, b, P);
+    if constexpr (LAYOUT == 0) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        a[p] = Elem<T>::to_f32(ALIGNED ? va.e[2 * p] : ea[2 * p]);
+        b[p] = Elem<T>::to_f32(ALIGNED ? va.e[2 * p + 1] : ea[2 * p + 1]);
+      }
     } else {
-      a[0] = Elem<T>::to_f32(xr[j]);
-      b[0] = Elem<T>::to_f32(xr[half + j]);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        a[p] = Elem<T>::to_f32(ALIGNED ? va.e[p] : ea[p]);
+        b[p] = Elem<T>::to_f32(ALIGNED ? vb.e[p] : eb[p]);
+      }
     }
     float oa[P], ob[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int i = j * P + p;
-      const float c = cr[i];
-      const float sn = sign * sr[i];
-      oa[p] = a[p] * c - b[p] * sn;
-      ob[p] = a[p] * sn + b[p] * c;
+      const float sn = sign * s[p];
+      oa[p] = a[p] * c[p] - b[p] * sn;
+      ob[p] = a[p] * sn + b[p] * c[p];
     }
-    if constexpr (ALIGNED) {
-      store_f32<T, true, NT>(yr + j * P, oa, P);
-      store_f32<T, true, NT>(yr + half + j * P, ob, P);
+    if constexpr (LAYOUT == 0) {
+      float o[V];
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        o[2 * p] = oa[p];
+        o[2 * p + 1] = ob[p];
+      }
+      if constexpr (ALIGNED) {
+        store_f32<T, true, NT>(ya, o, V);
+      } else {
+        ya[0] = Elem<T>::from_f32(o[0]);
+        ya[1] = Elem<T>::from_f32(o[1]);
+      }
     } else {
-      yr[j] = Elem<T>::from_f32(oa[0]);
-      yr[half + j] = Elem<T>::from_f32(ob[0]);
+      if constexpr (ALIGNED) {
+        store_f32<T, true, NT>(ya, oa, P);
+        store_f32<T, true, NT>(yb, ob, P);
+      } else {
+        ya[0] = Elem<T>::from_f32(oa[0]);
+        yb[0] = Elem<T>::from_f32(ob[0]);
+      }
     }
   }
-}
+};
+
+// A block covers 256 * kItemsPerThread items of one tensor: thread t takes items
+// base + t + 256 * u, all loaded before any is stored.  One item per thread measured best
+// on q [8, 2048, 32, 128] + k [8, 2048, 8, 128] bf16 (54.1 us; two 55.8, four 57.5): more
+// waves beat more loads per wave.
+constexpr int kItemsPerThread = 1;
 
 template <typename T, int LAYOUT, bool ALIGNED, bool NT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t0, RopeTensor t1, int head_dim,
@@ -128,9 +168,17 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeTensor t0, RopeTensor t1,
     b -= static_cast<uint32_t>(t0.blocks);
     t = &t1;
   }
-  const uint32_t item = b * 256u + threadIdx.x;
-  if (item >= t->items) return;
-  rope_item<T, LAYOUT, ALIGNED, NT>(*t, item, head_dim, cos_t, sin_t, sign);
+  const uint32_t base = b * (256u * kItemsPerThread) + threadIdx.x;
+  const uint32_t items = static_cast<uint32_t>(t->items);
+  RopeWork<T, LAYOUT, ALIGNED, NT> w[kItemsPerThread];
+#pragma unroll
+  for (int u = 0; u < kItemsPerThread; ++u) {
+    const uint32_t item = base + 256u * u;
+    if (item < items) w[u].load(*t, item, head_dim, cos_t, sin_t);
+  }
+#pragma unroll
+  for (int u = 0; u < kItemsPerThread; ++u)
+    if (base + 256u * u < items) w[u].store(sign);
 }
 
 bool parse(const void* x, void* y, const int64_t* d, int64_t head_dim, int64_t table_rows,
@@ -187,8 +235,9 @@ void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const 
   const int per_row = items_per_row<T, LAYOUT, ALIGNED>(head_dim);
   t0.items = t0.rows * per_row;
   t1.items = t1.rows * per_row;
-  t0.blocks = (t0.items + 255) / 256;
-  t1.blocks = (t1.items + 255) / 256;
+  constexpr int64_t kPerBlock = 256 * kItemsPerThread;
+  t0.blocks = (t0.items + kPerBlock - 1) / kPerBlock;
+  t1.blocks = (t1.items + kPerBlock - 1) / kPerBlock;
   const int64_t blocks = t0.blocks + t1.blocks;
   if (blocks == 0) return;
   // pt_rope has checked that (rows0 + rows1) * head_dim / 2 + 512 < 2^32, which bounds
