@@ -86,10 +86,10 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
   const float gs = SCALED ? *grad_scale : 1.0f;
   const int64_t start = (blk - r.first_block) * kBlockElems;
   const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
-  float* P = reinterpret_cast<float*>(r.p);
-  float* G = reinterpret_cast<float*>(r.g);
-  float* M = reinterpret_cast<float*>(r.m);
-  float* Vv = reinterpret_cast<float*>(r.v);
+  const gptr<float> P = as_global<float>(r.p);
+  const gptr<float> G = as_global<float>(r.g);
+  const gptr<float> M = as_global<float>(r.m);
+  const gptr<float> Vv = as_global<float>(r.v);
   const bool vec_ok = ((r.p | r.g | r.m | r.v) & 15) == 0;
 
   if (vec_ok && end - start == kBlockElems) {
@@ -97,10 +97,10 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
       const int64_t i = start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4;
-      pv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(P + i));
-      gv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(G + i));
-      mv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(M + i));
-      vv[k] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(Vv + i));
+      pv[k] = __builtin_nontemporal_load(reinterpret_cast<gptr<const f32x4>>(P + i));
+      gv[k] = __builtin_nontemporal_load(reinterpret_cast<gptr<const f32x4>>(G + i));
+      mv[k] = __builtin_nontemporal_load(reinterpret_cast<gptr<const f32x4>>(M + i));
+      vv[k] = __builtin_nontemporal_load(reinterpret_cast<gptr<const f32x4>>(Vv + i));
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
@@ -114,10 +114,10 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
         mv[k][j] = mm;
         vv[k][j] = v2;
       }
-      __builtin_nontemporal_store(pv[k], reinterpret_cast<f32x4*>(P + i));
-      __builtin_nontemporal_store(mv[k], reinterpret_cast<f32x4*>(M + i));
-      __builtin_nontemporal_store(vv[k], reinterpret_cast<f32x4*>(Vv + i));
-      if (SCALED && write_grad) __builtin_nontemporal_store(gv[k], reinterpret_cast<f32x4*>(G + i));
+      __builtin_nontemporal_store(pv[k], reinterpret_cast<gptr<f32x4>>(P + i));
+      __builtin_nontemporal_store(mv[k], reinterpret_cast<gptr<f32x4>>(M + i));
+      __builtin_nontemporal_store(vv[k], reinterpret_cast<gptr<f32x4>>(Vv + i));
+      if (SCALED && write_grad) __builtin_nontemporal_store(gv[k], reinterpret_cast<gptr<f32x4>>(G + i));
     }
   } else {
     for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
 constexpr int kWalkUnroll = 4;
 
 struct BlockSpan {
-  const float* g;
+  gptr<float> g;
   int64_t start, end;
   bool vec;  // a whole 16-byte-aligned block: one float4 per thread
 };
@@ -151,7 +151,7 @@ __device__ __forceinline__ BlockSpan block_span(const AdamRec* __restrict__ tabl
                                                 int64_t ntensors, int64_t vb) {
   const AdamRec r = table[find_tensor(table, ntensors, vb)];
   BlockSpan b;
-  b.g = reinterpret_cast<const float*>(r.g);
+  b.g = as_global<float>(r.g);
   b.start = (vb - r.first_block) * kBlockElems;
   b.end = (b.start + kBlockElems < r.n) ? b.start + kBlockElems : r.n;
   b.vec = (r.g & 15) == 0 && b.end - b.start == kBlockElems;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void grad_stats_kernel(const AdamRec* __r
         sp[u] = block_span(table, ntensors, base + u);
         if (sp[u].vec)
           gv[u] = __builtin_nontemporal_load(
-              reinterpret_cast<const f32x4*>(sp[u].g + sp[u].start + threadIdx.x * 4));
+              reinterpret_cast<gptr<const f32x4>>(sp[u].g + sp[u].start + threadIdx.x * 4));
       }
     }
 #pragma unroll
@@ -282,16 +282,16 @@ __global__ __launch_bounds__(kThreads) void grad_scale_kernel(const AdamRec* __r
         sp[u] = block_span(table, ntensors, base + u);
         if (sp[u].vec)
           gv[u] = __builtin_nontemporal_load(
-              reinterpret_cast<const f32x4*>(sp[u].g + sp[u].start + threadIdx.x * 4));
+              reinterpret_cast<gptr<const f32x4>>(sp[u].g + sp[u].start + threadIdx.x * 4));
       }
     }
 #pragma unroll
     for (int u = 0; u < kWalkUnroll; ++u) {
-      float* G = const_cast<float*>(sp[u].g);
+      const gptr<float> G = sp[u].g;
       if (sp[u].vec) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) gv[u][j] = gv[u][j] * s;
-        __builtin_nontemporal_store(gv[u], reinterpret_cast<f32x4*>(G + sp[u].start + threadIdx.x * 4));
+        __builtin_nontemporal_store(gv[u], reinterpret_cast<gptr<f32x4>>(G + sp[u].start + threadIdx.x * 4));
       } else {
         for (int64_t i = sp[u].start + threadIdx.x; i < sp[u].end; i += kThreads) G[i] = G[i] * s;
       }

@@ -150,6 +150,17 @@ __device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float v
   }
 }
 
+// Device memory reached through an address held as an integer (a record table) in the
+// global address space, so that the compiler emits global_* accesses: through a generic
+// pointer it would emit flat_* accesses, which also count against the LDS wait counter.
+template <typename T>
+using gptr = T __attribute__((address_space(1)))*;
+
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global(int64_t addr) {
+  return reinterpret_cast<gptr<T>>(addr);
+}
+
 // ------------------------------------------------------------------ reductions
 
 // Wave reductions on DPP lane moves (register-to-register, a few cycles each) instead of
