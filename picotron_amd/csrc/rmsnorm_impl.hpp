@@ -334,16 +334,27 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     load(a, ra);
     process(a, ra, 0);
   } else {
+    // Unconditional prefetches inside the loop, the last one or two rows peeled (as in the
+    // backward: a prefetch under a branch makes the compiler wait for it at the join).
     Row a, b;
     load(a, ra);
-    for (int it = 0; it < iters; it += 2) {
+    int it = 0;
+    for (; it + 2 < iters; it += 2) {
       const int64_t rb = ra + group_stride;
-      if (it + 1 < iters) load(b, rb);
+      load(b, rb);
       process(a, ra, 0);
       const int64_t rc = rb + group_stride;
-      if (it + 2 < iters) load(a, rc);
-      if (it + 1 < iters) process(b, rb, 1);
+      load(a, rc);
+      process(b, rb, 1);
       ra = rc;
+    }
+    if (it + 1 < iters) {
+      const int64_t rb = ra + group_stride;
+      load(b, rb);
+      process(a, ra, 0);
+      process(b, rb, 1);
+    } else {
+      process(a, ra, 0);
     }
   }
 }
