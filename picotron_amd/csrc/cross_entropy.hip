@@ -101,12 +101,12 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
   }
 }
 
-// Common start of both row kernels: locates the row and its target.  An ignored row (target
-// == ignore_index, or a position i >= valid_inner that has no target) gets a zero gradient
-// and a zero loss, and the function returns false.  Otherwise thread 0 reads
-// the target logit into *s_target_logit (NaN for a target outside [0, vocab), which also
-// sets status bit 0) before any thread of the block can overwrite the row: the block
-// passes at least two barriers before its first gradient store.
+// Start of the streaming row kernel: locates the row and its target.  An ignored row
+// (target == ignore_index, or a position i >= valid_inner that has no target) gets a zero
+// gradient and a zero loss, and the function returns false.  Otherwise thread 0 reads the
+// target logit into *s_target_logit (NaN for a target outside [0, vocab), which also sets
+// status bit 0) before any thread of the block can overwrite the row: the block passes at
+// least two barriers before its first gradient store.
 template <typename T, int V, bool ALIGNED>
 __device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t valid_inner,
                                              int64_t os, int64_t is, int vocab,
@@ -175,8 +175,7 @@ __device__ __forceinline__ RowRef row_ref(int64_t row, int64_t inner, int64_t va
 
 // Raw buffer resource (stride 0) over `bytes` bytes at `base`: the hardware drops loads
 // past the end (they return 0) and stores past the end, so a row's ragged last vectors need
-// no branches, and a resource of 0 bytes turns a row's loads into no-ops without memory
-// traffic.  The range check covers the VGPR offset plus the instruction's immediate offset
+// no branches.  The range check covers the VGPR offset plus the instruction's immediate offset
 // but not the SGPR offset, so every access below puts its whole offset in the VGPR operand
 // and passes an SGPR offset of 0.  kBufferWord3 is the gfx9-family data-format word for
 // untyped 32-bit access.
