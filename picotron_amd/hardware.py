@@ -5,6 +5,10 @@
 ``TritonReport`` fields: ``installed`` means the HIP kernel library loads,
 ``hardware_compatible`` means the device is a gfx950 GPU, and ``available`` requires both
 plus ``enabled``.  Never enables anything implicitly.
+
+``kernel_status_rows(flags)`` gives the two kernel rows of the run banner
+(src/picotron/logging/display.py:315-338) from the live state rather than the reference's
+fixed "rmsnorm=real swiglu=real rope=fallback ..." string.
 """
 
 from __future__ import annotations
@@ -47,3 +51,32 @@ def detect_triton_support(
         hardware_compatible=hardware_compatible,
         available=enabled and installed and hardware_compatible,
     )
+
+
+# Kernels of the run banner, in its order; attention has no fused kernel here.
+_BANNER_KERNELS = ("rmsnorm", "swiglu", "rope", "attention", "cross_entropy", "adamw")
+
+
+def kernel_status_rows(
+    flags, *, device: int | torch.device | None = None
+) -> tuple[tuple[str, str], tuple[str, str]]:
+    """The banner's ``("Triton kernels", ...)`` and ``("Triton status", ...)`` rows for a
+    ``TritonKernelsConfig`` (display.py:315-338): "off" when no flag is set, "active: ..."
+    when the enabled kernels run on the HIP library, "requested; fallback: ..." when they
+    cannot; the status row says per kernel whether the HIP kernel ("real") or the PyTorch
+    fallback would run."""
+
+    enabled = tuple(name for name in _BANNER_KERNELS if getattr(flags, name))
+    report = detect_triton_support(enabled=bool(enabled), device=device)
+    if not enabled:
+        kernels = "off"
+    elif report.available:
+        kernels = "active: " + ", ".join(enabled)
+    else:
+        kernels = "requested; fallback: " + ", ".join(enabled)
+    runs = report.installed and report.hardware_compatible
+    status = " ".join(
+        f"{name}={'real' if runs and name != 'attention' else 'fallback'}"
+        for name in _BANNER_KERNELS
+    )
+    return ("Triton kernels", kernels), ("Triton status", status)

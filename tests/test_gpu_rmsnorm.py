@@ -193,3 +193,13 @@ def test_autograd_surface_and_module(gpu):
     assert not norm._triton_fallback_warned
     ref, _ = o_rms.forward(x.detach().float(), norm.weight.detach(), norm.eps)
     close_fp32(out, ref)
+
+
+def test_banner_rows_report_the_hip_kernels(gpu):
+    from picotron_amd.config import TritonKernelsConfig
+    from picotron_amd.hardware import kernel_status_rows
+
+    rows = kernel_status_rows(TritonKernelsConfig(rmsnorm=True, swiglu=True), device=gpu)
+    assert rows[0] == ("Triton kernels", "active: rmsnorm, swiglu")
+    assert rows[1] == ("Triton status", "rmsnorm=real swiglu=real rope=real "
+                       "attention=fallback cross_entropy=real adamw=real")

@@ -13,7 +13,7 @@ from torch.nn import functional as F
 from torch.optim import AdamW
 
 from picotron_amd.config import ConfigValidationError, TritonKernelsConfig
-from picotron_amd.hardware import detect_triton_support
+from picotron_amd.hardware import detect_triton_support, kernel_status_rows
 from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU, apply_rotary_embedding, rotary_cos_sin
 from picotron_amd.nn.rope import apply_rotary_embedding_rotate_half
 from picotron_amd.nn.triton_kernels import (
@@ -220,6 +220,16 @@ def test_detect_triton_support_on_cpu():
     report = detect_triton_support()
     assert not report.enabled and not report.available and not report.hardware_compatible
     assert not detect_triton_support(enabled=True).available
+
+
+def test_banner_rows_on_cpu():
+    # the two kernel rows of the run banner (display.py:315-338), from the live state
+    off = kernel_status_rows(TritonKernelsConfig())
+    assert off[0] == ("Triton kernels", "off")
+    assert off[1] == ("Triton status", "rmsnorm=fallback swiglu=fallback rope=fallback "
+                      "attention=fallback cross_entropy=fallback adamw=fallback")
+    asked = kernel_status_rows(TritonKernelsConfig(rmsnorm=True, adamw=True))
+    assert asked[0] == ("Triton kernels", "requested; fallback: rmsnorm, adamw")
 
 
 def test_kernel_flags_are_strict_bools():
