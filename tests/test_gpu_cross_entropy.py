@@ -94,6 +94,26 @@ def test_shapes(gpu, dtype, rows, vocab):
 
 @pytest.mark.parametrize(
     "dtype,vocab",
+    [(torch.bfloat16, 24), (torch.bfloat16, 50264), (torch.float16, 50264), (torch.bfloat16, 128256),
+     (torch.float16, 128256), (torch.float32, 65528), (torch.float32, 12)],
+)
+def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
+    # 16-byte aligned rows held in registers whose last chunk of vectors is only partly
+    # inside the row: targets at the first and last logit, at the first element of the last
+    # chunk and of the vector before it, and an ignored row.
+    v = 16 // torch.tensor([], dtype=dtype).element_size()
+    per_thread = -(-vocab // (1024 * v))  # chunks of 1024 vectors that hold logits
+    last_chunk = (per_thread - 1) * 1024 * v  # first logit of the chunk holding the last one
+    picks = [0, vocab - 1, last_chunk, max(last_chunk - v, 0), -100, vocab // 2]
+    # every target is a valid index (the oracle's gather on the GPU does not check bounds)
+    assert all(p == -100 or 0 <= p < vocab for p in picks)
+    logits = randn((len(picks), vocab), dtype, gpu, vocab + 11, 2.0)
+    targets = torch.tensor(picks, device=gpu)
+    _check(logits, targets, dtype)
+
+
+@pytest.mark.parametrize(
+    "dtype,vocab",
     [(torch.bfloat16, 4096), (torch.bfloat16, 262144), (torch.float32, 1001), (torch.float16, 50257)],
 )
 def test_masked_logits(gpu, dtype, vocab):
