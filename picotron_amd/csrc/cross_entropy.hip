@@ -16,8 +16,9 @@
 //      softmax / n_valid is written from registers with one multiply per element and no
 //      second exponential: HBM sees one read and one write of the logits.  The target
 //      element's gradient (softmax_t - 1) / n_valid comes from the exact fp32 target logit.
-//      Rows too long for registers, or not 16-byte aligned, use ce_rows_stream (online
-//      max / sum, then a second read).  Each row's fp32 loss goes to the workspace.
+//      Longer aligned rows use ce_rows_batched (two passes, batches of loads in flight, the
+//      second pass served largely by the Infinity Cache); unaligned rows ce_rows_stream.
+//      Each row's fp32 loss goes to the workspace.
 //   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
 //      n_valid, so the loss is bitwise reproducible.
 // exp(x - m) is evaluated as exp2((x - m) * log2(e)) on the hardware exp2 unit.
@@ -344,9 +345,128 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
 }
 
-// Rows too long for registers, or not 16-byte aligned: pass 1 streams the row once with an
-// online max / sum-exp per thread; pass 2 re-reads it (largely from L2 / MALL) to write the
-// gradient.
+// Aligned rows too long for registers (row_bytes + kStreamBatchBytes < 2^31): one 1024-thread
+// workgroup per row in two passes of batches of kStreamBatch 16-byte vectors per thread,
+// loaded together with raw buffer loads (the hardware range check drops the ragged end).
+//   1. cached loads (the row stays in the Infinity Cache for pass 2) and an online max /
+//      sum per thread, reduced as in ce_rows_kernel (one barrier);
+//   2. the row re-read (nontemporal: last use), exp(x - M) / (S * n_valid) written over it;
+//      the thread holding the target stores (softmax_t - 1) / n_valid after its own vector.
+constexpr int kStreamBatch = 4;
+constexpr int kStreamBatchBytes = kStreamBatch * kThreads * 16;
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
+    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
+    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
+  constexpr int V = Elem<T>::VEC;
+  constexpr int kChunkBytes = kThreads * 16;
+  __shared__ float red_m[kWaves];
+  __shared__ float red_s[kWaves];
+  __shared__ float s_xt;
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64;
+  const int64_t row = blockIdx.x;
+  const int row_bytes = vocab * static_cast<int>(sizeof(T));
+  const int voff = tid * 16;
+  const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
+  T* p = logits + cur.off;
+  const auto buf = row_buffer(p, row_bytes);
+
+  if (cur.skip) {
+    if (write_grad) {
+      for (int b = 0; b < row_bytes; b += kChunkBytes)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf, voff + b, 0,
+                                               kNonTemporal);
+    }
+    if (tid == 0) row_losses(ws)[row] = 0.0f;
+    return;
+  }
+  const bool bad = cur.tgt < 0 || cur.tgt >= vocab;
+  if (tid == 0) {
+    s_xt = bad ? NAN : Elem<T>::to_f32(p[cur.tgt]);
+    if (bad) atomicOr(&ws->status, 1);
+  }
+
+  float m = -INFINITY, s = 0.0f;
+  for (int b = 0; b < row_bytes; b += kStreamBatchBytes) {
+    Vec16<T> v[kStreamBatch];
+#pragma unroll
+    for (int u = 0; u < kStreamBatch; ++u)
+      v[u].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, voff + b + u * kChunkBytes, 0, 0);
+#pragma unroll
+    for (int u = 0; u < kStreamBatch; ++u) {
+      if (voff + b + u * kChunkBytes >= row_bytes) {
+        const uint32_t ninf = kNegInfWord<T>;
+        v[u].raw = u32x4{ninf, ninf, ninf, ninf};
+      }
+      float x[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(v[u].e[i]);
+      float cm = x[0];
+#pragma unroll
+      for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
+      const float nm = fmaxf(m, cm);
+      const float ref = nm == -INFINITY ? 0.0f : nm;
+      float add = 0.0f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) add += exp_shifted(x[i], ref);
+      s = s * exp_shifted(m, ref) + add;
+      m = nm;
+    }
+  }
+  const float mw = wave_max(m);
+  const float sw = wave_sum(s * exp_shifted(m, mw == -INFINITY ? 0.0f : mw));
+  if (lane == 0) {
+    red_m[wave] = mw;
+    red_s[wave] = sw;
+  }
+  __syncthreads();
+  float M = red_m[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, red_m[w]);
+  const float refM = M == -INFINITY ? 0.0f : M;
+  float S = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) S += red_s[w] * exp_shifted(red_m[w], refM);
+  const float xt = s_xt;
+  if (tid == 0) row_losses(ws)[row] = row_loss(M, S, xt);
+  if (!write_grad) return;
+
+  const float inv_n = inv_n_of(ws);
+  const float scale = inv_n / S;
+  for (int b = 0; b < row_bytes; b += kStreamBatchBytes) {
+    Vec16<T> v[kStreamBatch];
+#pragma unroll
+    for (int u = 0; u < kStreamBatch; ++u)
+      v[u].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, voff + b + u * kChunkBytes, 0,
+                                                       kNonTemporal);
+#pragma unroll
+    for (int u = 0; u < kStreamBatch; ++u) {
+      Vec16<T> out;
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        out.e[i] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(v[u].e[i]), M) * scale);
+      __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, voff + b + u * kChunkBytes, 0,
+                                             kNonTemporal);
+    }
+  }
+  if (!bad && tid == static_cast<int>((cur.tgt / V) % kThreads)) {
+    Vec16<T> one;
+    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n));
+    const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
+    if constexpr (sizeof(T) == 4) {
+      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
+                                            buf, toff, 0, kNonTemporal);
+    }
+  }
+}
+
+// Rows not 16-byte aligned (or aligned rows of 2^31 bytes and more): pass 1 streams the row
+// once with an online max / sum-exp per thread; pass 2 re-reads it to write the gradient.
 template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
     T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
@@ -503,6 +623,14 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
     PT_CE_CASE(8)
     PT_CE_CASE(16)
 #undef PT_CE_CASE
+    if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
+        (int64_t{1} << 31)) {
+      hipLaunchKernelGGL((ce_rows_batched_kernel<T>), dim3(static_cast<unsigned>(rows)),
+                         dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
+                         d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
+                         ws);
+      return;
+    }
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
                        d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,

@@ -82,7 +82,10 @@ def test_full_config_bf16(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows,vocab", [(1, 1), (5, 3), (7, 1000), (33, 8192), (4, 50257), (3, 131072), (2, 262144)])
+@pytest.mark.parametrize(
+    "rows,vocab",
+    [(1, 1), (5, 3), (7, 1000), (33, 8192), (4, 50257), (3, 131072), (3, 151936), (2, 248320), (2, 262144)],
+)
 def test_shapes(gpu, dtype, rows, vocab):
     logits = randn((rows, vocab), dtype, gpu, rows * 3 + vocab, 2.0)
     g = torch.Generator(device=gpu).manual_seed(vocab)
@@ -95,12 +98,13 @@ def test_shapes(gpu, dtype, rows, vocab):
 @pytest.mark.parametrize(
     "dtype,vocab",
     [(torch.bfloat16, 24), (torch.bfloat16, 50264), (torch.float16, 50264), (torch.bfloat16, 128256),
-     (torch.float16, 128256), (torch.float32, 65528), (torch.float32, 12)],
+     (torch.float16, 128256), (torch.float32, 65528), (torch.float32, 12), (torch.bfloat16, 151936),
+     (torch.float32, 65540)],
 )
 def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
-    # 16-byte aligned rows held in registers whose last chunk of vectors is only partly
-    # inside the row: targets at the first and last logit, at the first element of the last
-    # chunk and of the vector before it, and an ignored row.
+    # 16-byte aligned rows (held in registers, or streamed in batches when longer) whose last
+    # chunk of vectors is only partly inside the row: targets at the first and last logit,
+    # at the first element of the last chunk and of the vector before it, and an ignored row.
     v = 16 // torch.tensor([], dtype=dtype).element_size()
     per_thread = -(-vocab // (1024 * v))  # chunks of 1024 vectors that hold logits
     last_chunk = (per_thread - 1) * 1024 * v  # first logit of the chunk holding the last one
