@@ -16,8 +16,8 @@
 //      softmax / n_valid is written from registers with one multiply per element and no
 //      second exponential: HBM sees one read and one write of the logits.  The target
 //      element's gradient (softmax_t - 1) / n_valid comes from the exact fp32 target logit.
-//      Longer aligned rows use ce_rows_batched (two passes, batches of loads in flight, the
-//      second pass served largely by the Infinity Cache); unaligned rows ce_rows_stream.
+//      Longer or unaligned rows use ce_rows_batched (two passes, batches of loads in flight,
+//      the second pass served largely by the Infinity Cache).
 //      Each row's fp32 loss goes to the workspace.
 //   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
 //      n_valid, so the loss is bitwise reproducible.
@@ -345,13 +345,16 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
 }
 
-// Aligned rows too long for registers (row_bytes + kStreamBatchBytes < 2^31): one 1024-thread
-// workgroup per row in two passes of batches of kStreamBatch 16-byte vectors per thread,
-// loaded together with raw buffer loads (the hardware range check drops the ragged end).
+// Rows that the register-resident kernel does not take -- longer than it holds, or not
+// 16-byte aligned -- with row_bytes + kStreamBatchBytes < 2^31: one 1024-thread workgroup
+// per row in two passes.  A row is split into a head of up to V-1 elements before its first
+// 16-byte boundary (one per thread, from thread 0), a body of 16-byte vectors read in
+// batches of kStreamBatch per thread with raw buffer loads (the hardware range check drops
+// the ragged end), and a tail of up to V-1 elements (one per thread, from the last thread).
 //   1. cached loads (the row stays in the Infinity Cache for pass 2) and an online max /
 //      sum per thread, reduced as in ce_rows_kernel (one barrier);
 //   2. the row re-read (nontemporal: last use), exp(x - M) / (S * n_valid) written over it;
-//      the thread holding the target stores (softmax_t - 1) / n_valid after its own vector.
+//      the thread that wrote the target's element then stores (softmax_t - 1) / n_valid.
 constexpr int kStreamBatch = 4;
 constexpr int kStreamBatchBytes = kStreamBatch * kThreads * 16;
 
@@ -368,17 +371,26 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
   const int64_t row = blockIdx.x;
-  const int row_bytes = vocab * static_cast<int>(sizeof(T));
-  const int voff = tid * 16;
   const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
   T* p = logits + cur.off;
-  const auto buf = row_buffer(p, row_bytes);
+  // head [0, head), body [head, head + nbody * V), tail [head + nbody * V, vocab)
+  const int lead = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T));
+  const int head = lead < vocab ? lead : vocab;
+  const int nbody = (vocab - head) / V;
+  const int tail_start = head + nbody * V;
+  const int ntail = vocab - tail_start;
+  const int body_bytes = nbody * 16;
+  const auto buf = row_buffer(p + head, body_bytes);
+  const int voff = tid * 16;
+  // the one head or tail element of this thread, if any
+  const int my_edge = tid < head ? tid : (kThreads - 1 - tid < ntail ? tail_start + (kThreads - 1 - tid) : -1);
 
   if (cur.skip) {
     if (write_grad) {
-      for (int b = 0; b < row_bytes; b += kChunkBytes)
+      for (int b = 0; b < body_bytes; b += kChunkBytes)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf, voff + b, 0,
                                                kNonTemporal);
+      if (my_edge >= 0) p[my_edge] = Elem<T>::from_f32(0.0f);
     }
     if (tid == 0) row_losses(ws)[row] = 0.0f;
     return;
@@ -390,14 +402,18 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   }
 
   float m = -INFINITY, s = 0.0f;
-  for (int b = 0; b < row_bytes; b += kStreamBatchBytes) {
+  if (my_edge >= 0) {
+    m = Elem<T>::to_f32(p[my_edge]);
+    s = m == -INFINITY ? 0.0f : 1.0f;  // exp(x - x); a lone -inf contributes nothing
+  }
+  for (int b = 0; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
       v[u].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, voff + b + u * kChunkBytes, 0, 0);
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u) {
-      if (voff + b + u * kChunkBytes >= row_bytes) {
+      if (voff + b + u * kChunkBytes >= body_bytes) {
         const uint32_t ninf = kNegInfWord<T>;
         v[u].raw = u32x4{ninf, ninf, ninf, ninf};
       }
@@ -436,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
 
   const float inv_n = inv_n_of(ws);
   const float scale = inv_n / S;
-  for (int b = 0; b < row_bytes; b += kStreamBatchBytes) {
+  for (int b = 0; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
@@ -452,21 +468,36 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
                                              kNonTemporal);
     }
   }
-  if (!bad && tid == static_cast<int>((cur.tgt / V) % kThreads)) {
-    Vec16<T> one;
-    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n));
-    const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
-    if constexpr (sizeof(T) == 4) {
-      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
-    } else {
-      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
-                                            buf, toff, 0, kNonTemporal);
+  if (my_edge >= 0) p[my_edge] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(p[my_edge]), M) * scale);
+  if (!bad) {
+    // The owner rewrites the target over its own earlier store of that element, through the
+    // same kind of access (buffer store for the body, plain store for head and tail), so the
+    // two stay in program order.
+    const int t = static_cast<int>(cur.tgt);
+    const bool in_body = t >= head && t < tail_start;
+    const int owner = t < head ? t : (in_body ? ((t - head) / V) % kThreads
+                                              : kThreads - 1 - (t - tail_start));
+    if (tid == owner) {
+      const T gt = Elem<T>::from_f32(target_grad(M, S, xt, inv_n));
+      if (in_body) {
+        Vec16<T> one;
+        one.e[0] = gt;
+        const int toff = (t - head) * static_cast<int>(sizeof(T));
+        if constexpr (sizeof(T) == 4) {
+          __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
+                                                buf, toff, 0, kNonTemporal);
+        }
+      } else {
+        p[t] = gt;
+      }
     }
   }
 }
 
-// Rows not 16-byte aligned (or aligned rows of 2^31 bytes and more): pass 1 streams the row
-// once with an online max / sum-exp per thread; pass 2 re-reads it to write the gradient.
+// Rows of 2^31 bytes and more: pass 1 streams the row once with an online max / sum-exp per
+// thread; pass 2 re-reads it to write the gradient.
 template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
     T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
@@ -605,7 +636,8 @@ void launch_rows(const CeRows& d, int write_grad, CeWork* ws, int64_t rows, hipS
 }
 
 // Register-resident rows for up to 16 vectors per thread (131072 fp16/bf16 or 65536 fp32
-// elements); longer or unaligned rows stream.
+// elements) when every row is 16-byte aligned; other rows take the batched two-pass kernel
+// (the element-wise stream only for rows of 2 GB and more).
 template <typename T>
 void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, int64_t rows,
                    hipStream_t st) {
@@ -623,14 +655,14 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
     PT_CE_CASE(8)
     PT_CE_CASE(16)
 #undef PT_CE_CASE
-    if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
-        (int64_t{1} << 31)) {
-      hipLaunchKernelGGL((ce_rows_batched_kernel<T>), dim3(static_cast<unsigned>(rows)),
-                         dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
-                         d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
-                         ws);
-      return;
-    }
+  }
+  if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
+      (int64_t{1} << 31)) {
+    hipLaunchKernelGGL((ce_rows_batched_kernel<T>), dim3(static_cast<unsigned>(rows)),
+                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
+                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
+                       ws);
+  } else if (aligned) {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
                        d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,

@@ -116,6 +116,27 @@ def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
     _check(logits, targets, dtype)
 
 
+@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 50257), (torch.float16, 50257), (torch.float32, 1001)])
+def test_targets_at_the_splits_of_unaligned_rows(gpu, dtype, vocab):
+    # Rows whose byte stride is not a multiple of 16 start at varying alignments; each is
+    # split into a head before its first 16-byte boundary, a body of 16-byte vectors and a
+    # tail.  Targets sit on both sides of each split and at the ends of the row.
+    es = torch.tensor([], dtype=dtype).element_size()
+    v = 16 // es
+    rows = 16
+    logits = randn((rows, vocab), dtype, gpu, vocab + 13, 2.0)
+    picks = []
+    for r in range(rows):
+        addr = logits.data_ptr() + r * vocab * es
+        head = min(((16 - addr % 16) % 16) // es, vocab)
+        tail_start = head + (vocab - head) // v * v
+        candidates = [head - 1, head, tail_start - 1, tail_start, 0, vocab - 1]
+        picks.append([c for c in candidates if 0 <= c < vocab][r % 4])
+    picks[5] = -100
+    assert all(p == -100 or 0 <= p < vocab for p in picks)
+    _check(logits, torch.tensor(picks, device=gpu), dtype)
+
+
 @pytest.mark.parametrize(
     "dtype,vocab",
     [(torch.bfloat16, 4096), (torch.bfloat16, 262144), (torch.float32, 1001), (torch.float16, 50257)],
