@@ -577,9 +577,10 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
 
 // In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1.
 // Ignored rows stay zero whatever the scalar is (torch's nll_loss backward leaves them 0).
-// The work items are (row, chunk of 1024 vectors or elements); a grid of a few blocks per CU
-// walks them, so the common grad_output == 1 case costs one small launch.  ALIGNED rows
-// move 16-byte vectors (4 per thread per chunk), otherwise single elements.
+// The work items are (row, chunk of 1024 vectors or elements); a grid of up to 128 blocks
+// per CU walks them (a one-shot grid streams no faster and makes the common
+// grad_output == 1 launch several times dearer).  ALIGNED rows move 16-byte vectors (4 per
+// thread per chunk), nontemporal (touched once), otherwise single elements.
 constexpr int kScaleVecs = 4;
 
 template <typename T, bool ALIGNED>
@@ -607,10 +608,10 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
       if (e < vocab) {
         if constexpr (ALIGNED) {
           float x[V];
-          load_f32<T, true>(p + e, x, V);
+          load_f32<T, true, true>(p + e, x, V);
 #pragma unroll
           for (int i = 0; i < V; ++i) x[i] *= sc;
-          store_f32<T, true>(p + e, x, V);
+          store_f32<T, true, true>(p + e, x, V);
         } else {
           p[e] = Elem<T>::from_f32(Elem<T>::to_f32(p[e]) * sc);
         }
@@ -719,7 +720,7 @@ void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, hi
   constexpr int64_t kChunk = 256 * (ALIGNED ? Elem<T>::VEC : 1) * kScaleVecs;
   const int64_t chunks = (d.vocab + kChunk - 1) / kChunk;
   const int64_t items = rows * chunks;
-  const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
+  const int64_t cap = static_cast<int64_t>(num_cus()) * 128;
   const unsigned grid = static_cast<unsigned>(items < cap ? items : cap);
   hipLaunchKernelGGL((ce_scale_kernel<T, ALIGNED>), dim3(grid), dim3(256), 0, st,
                      static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is, d.vocab, items,
