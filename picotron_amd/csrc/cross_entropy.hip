@@ -357,8 +357,12 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
 //      the thread that wrote the target's element then stores (softmax_t - 1) / n_valid.
 constexpr int kStreamBatch = 4;
 constexpr int kStreamBatchBytes = kStreamBatch * kThreads * 16;
+// Leading body chunks (1024 vectors each) held in registers as exps between the passes, as
+// in ce_rows_kernel: only the body beyond them is read twice (at most kKeepChunks; the
+// launch keeps fewer for short rows).
+constexpr int kKeepChunks = 12;
 
-template <typename T>
+template <typename T, int KEEP>
 __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
     int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
@@ -395,6 +399,10 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     if (tid == 0) row_losses(ws)[row] = 0.0f;
     return;
   }
+  Vec16<T> kv[KEEP];
+#pragma unroll
+  for (int k = 0; k < KEEP; ++k)
+    kv[k].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, voff + k * kChunkBytes, 0, kNonTemporal);
   const bool bad = cur.tgt < 0 || cur.tgt >= vocab;
   if (tid == 0) {
     s_xt = bad ? NAN : Elem<T>::to_f32(p[cur.tgt]);
@@ -406,7 +414,35 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     m = Elem<T>::to_f32(p[my_edge]);
     s = m == -INFINITY ? 0.0f : 1.0f;  // exp(x - x); a lone -inf contributes nothing
   }
-  for (int b = 0; b < body_bytes; b += kStreamBatchBytes) {
+  float mk[KEEP];  // running max after kept chunk k: the reference of its exps
+#pragma unroll
+  for (int k = 0; k < KEEP; ++k) {
+    Vec16<T> r = kv[k];
+    if (voff + k * kChunkBytes >= body_bytes) {
+      const uint32_t ninf = kNegInfWord<T>;
+      r.raw = u32x4{ninf, ninf, ninf, ninf};
+    }
+    float x[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
+    float cm = x[0];
+#pragma unroll
+    for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
+    const float nm = fmaxf(m, cm);
+    const float ref = nm == -INFINITY ? 0.0f : nm;
+    float add = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float e = exp_shifted(x[i], ref);
+      add += e;
+      kv[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+    }
+    asm volatile("" : "+v"(kv[k].raw));  // packed here, not carried as fp32 across the barrier
+    s = s * exp_shifted(m, ref) + add;
+    m = nm;
+    mk[k] = nm;
+  }
+  for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
@@ -452,7 +488,18 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
 
   const float inv_n = inv_n_of(ws);
   const float scale = inv_n / S;
-  for (int b = 0; b < body_bytes; b += kStreamBatchBytes) {
+#pragma unroll
+  for (int k = 0; k < KEEP; ++k) {
+    // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf
+    const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
+    Vec16<T> out;
+#pragma unroll
+    for (int i = 0; i < V; ++i) out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(kv[k].e[i]) * f);
+    int vo = voff + k * kChunkBytes;
+    asm volatile("" : "+v"(vo));
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, vo, 0, kNonTemporal);
+  }
+  for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
@@ -659,10 +706,25 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
   }
   if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
       (int64_t{1} << 31)) {
-    hipLaunchKernelGGL((ce_rows_batched_kernel<T>), dim3(static_cast<unsigned>(rows)),
-                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
-                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
-                       ws);
+    // Rows whose body fits in 1, 2, 4 or 8 kept chunks are read once; longer rows keep
+    // kKeepChunks and stream the rest twice.  Fewer kept chunks leave room for two
+    // workgroups per CU.
+#define PT_CE_BATCHED(K)                                                                       \
+  hipLaunchKernelGGL((ce_rows_batched_kernel<T, K>), dim3(static_cast<unsigned>(rows)),       \
+                     dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner, \
+                     d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws)
+    if (per_thread <= 1) {
+      PT_CE_BATCHED(1);
+    } else if (per_thread <= 2) {
+      PT_CE_BATCHED(2);
+    } else if (per_thread <= 4) {
+      PT_CE_BATCHED(4);
+    } else if (per_thread <= 8) {
+      PT_CE_BATCHED(8);
+    } else {
+      PT_CE_BATCHED(kKeepChunks);
+    }
+#undef PT_CE_BATCHED
   } else if (aligned) {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
