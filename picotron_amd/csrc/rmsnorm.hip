@@ -60,7 +60,8 @@ int validate(const char* fn, int64_t rows, int64_t cols, int xdt, int wdt, bool 
   // Bounds the per-block row-group count (an int) for any grid.
   if (rows > (int64_t{1} << 36)) return fail(PT_EUNSUPPORTED, std::string(fn) + ": rows too large");
   const int vec = 16 / dtype_size(xdt);
-  const int cap = cap_of(backward ? tuning().bwd_vpl_cap : tuning().fwd_vpl_cap);
+  const int cap = cap_of(backward ? bwd_vpl_cap_for(tuning().bwd_vpl_cap, cols, vec)
+                                  : tuning().fwd_vpl_cap);
   if (!choose_shape(cols, vec, cap, s))
     return fail(PT_EUNSUPPORTED, std::string(fn) + ": hidden size " + std::to_string(cols) +
                                      " exceeds the register-resident row capacity (" +
@@ -216,7 +217,8 @@ size_t pt_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols, int x_dtype) {
   Shape s;
   if (rows <= 0 || cols <= 0 || !valid_dtype(x_dtype)) return 0;
   const int vec = 16 / dtype_size(x_dtype);
-  if (!choose_shape(cols, vec, cap_of(tuning().bwd_vpl_cap), &s)) return 0;
+  if (!choose_shape(cols, vec, cap_of(bwd_vpl_cap_for(tuning().bwd_vpl_cap, cols, vec)), &s))
+    return 0;
   // Enough for either path (aligned shape or the unaligned subset).
   int64_t blocks = bwd_blocks(rows, s);
   const int64_t ublocks = bwd_blocks(rows, unaligned_shape(cols, vec));
