@@ -1,0 +1,148 @@
+"""One training step of a small Llama-style decoder built from this package's modules, with
+every fused kernel switched on, against the same model on the reference's PyTorch
+fallbacks (the drop-in contract end to end).
+
+The model follows the reference decoder's structure (src/picotron/models/picotron_decoder.py:
+input norm, attention with RoPE, residual add, MLP norm, SwiGLU MLP, residual add, final
+norm, LM head), the loss is the train loop's next-token cross-entropy
+(src/picotron/training/train_loop.py:141-144) and the step is gradient clipping plus AdamW
+(train_loop.py:163-168, 338-350).  Only the kernels differ between the two runs; attention
+and the linear layers are plain PyTorch in both.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import warnings
+
+import pytest
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU
+from picotron_amd.nn.triton_kernels import AdamWStepWithFallback, CrossEntropyWithFallback
+
+pytestmark = pytest.mark.gpu
+
+VOCAB, HIDDEN, INTER, HEADS, KV_HEADS, LAYERS = 512, 128, 384, 4, 2, 2
+HEAD_DIM = HIDDEN // HEADS
+
+
+class Block(nn.Module):
+    def __init__(self, fused: bool) -> None:
+        super().__init__()
+        self.input_norm = RMSNorm(HIDDEN, use_triton_rmsnorm=fused)
+        self.q = nn.Linear(HIDDEN, HEADS * HEAD_DIM, bias=False)
+        self.k = nn.Linear(HIDDEN, KV_HEADS * HEAD_DIM, bias=False)
+        self.v = nn.Linear(HIDDEN, KV_HEADS * HEAD_DIM, bias=False)
+        self.o = nn.Linear(HEADS * HEAD_DIM, HIDDEN, bias=False)
+        self.rope = RotaryEmbedding(HEAD_DIM, 500_000.0, use_triton_rope=fused)
+        self.mlp_norm = RMSNorm(HIDDEN, use_triton_rmsnorm=fused)
+        self.mlp = SwiGLU(HIDDEN, INTER, use_triton_swiglu=fused)
+
+    def attention(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, _ = x.shape
+        q = self.q(x).view(b, s, HEADS, HEAD_DIM).transpose(1, 2)
+        k = self.k(x).view(b, s, KV_HEADS, HEAD_DIM).transpose(1, 2)
+        v = self.v(x).view(b, s, KV_HEADS, HEAD_DIM).transpose(1, 2)
+        q, k = self.rope(q, k)
+        rep = HEADS // KV_HEADS
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+        out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
+        return self.o(out.to(x.dtype).transpose(1, 2).reshape(b, s, HEADS * HEAD_DIM))
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        # the reference's `hidden + attention(...)` promotes the autocast output to the
+        # residual stream's fp32; the fused add takes it already promoted
+        attn = self.attention(self.input_norm(hidden)).to(hidden.dtype)
+        hidden, normed = self.mlp_norm.add_and_norm(attn, hidden)
+        return hidden + self.mlp(normed)
+
+
+class Decoder(nn.Module):
+    def __init__(self, fused: bool) -> None:
+        super().__init__()
+        self.embed = nn.Embedding(VOCAB, HIDDEN)
+        self.blocks = nn.ModuleList(Block(fused) for _ in range(LAYERS))
+        self.final_norm = RMSNorm(HIDDEN, use_triton_rmsnorm=fused)
+        self.head = nn.Linear(HIDDEN, VOCAB, bias=False)
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        hidden = self.embed(ids)
+        for block in self.blocks:
+            hidden = block(hidden)
+        return self.head(self.final_norm(hidden))
+
+
+def _models(gpu):
+    torch.manual_seed(7)
+    reference = Decoder(fused=False).to(gpu)
+    with torch.no_grad():
+        for module in reference.modules():
+            if isinstance(module, RMSNorm):
+                module.weight.add_(0.05 * torch.randn_like(module.weight))
+    fused = Decoder(fused=True).to(gpu)
+    fused.load_state_dict(reference.state_dict())
+    return reference, fused
+
+
+def _step(model, fused: bool, ids, *, eps: float, autocast: bool):
+    optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), eps=eps,
+                                  weight_decay=0.1, foreach=False)
+    loss_fn = CrossEntropyWithFallback(use_triton=fused)
+    stepper = AdamWStepWithFallback(use_triton=fused)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        logits = model(ids)
+        loss = loss_fn(logits, ids, shift=True)
+    loss.backward()
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters()}
+    stepper.step(optimizer, max_grad_norm=1.0)
+    return loss.detach(), grads, optimizer
+
+
+def test_fp32_training_step_matches_the_fallback_model(gpu):
+    reference, fused = _models(gpu)
+    ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(3)).to(gpu)
+    with _no_fallback_warning():
+        loss_f, grads_f, opt_f = _step(fused, True, ids, eps=1e-3, autocast=False)
+    loss_r, grads_r, opt_r = _step(reference, False, ids, eps=1e-3, autocast=False)
+    assert abs(loss_f.item() - loss_r.item()) <= 1e-5 * abs(loss_r.item())
+    for name, g in grads_r.items():
+        scale = float(g.abs().max())
+        torch.testing.assert_close(grads_f[name], g, rtol=1e-4, atol=1e-5 * scale, msg=name)
+    # after clipping (written back into .grad) and the AdamW step
+    for (name, p_f), p_r in zip(fused.named_parameters(), reference.parameters()):
+        torch.testing.assert_close(p_f.grad, p_r.grad, rtol=1e-4, atol=1e-5 * float(p_r.grad.abs().max()),
+                                   msg=f"clipped {name}")
+        torch.testing.assert_close(p_f.detach(), p_r.detach(), rtol=1e-5, atol=1e-7, msg=name)
+        st_f, st_r = opt_f.state[p_f], opt_r.state[p_r]
+        assert float(st_f["step"]) == float(st_r["step"]) == 1.0
+        torch.testing.assert_close(st_f["exp_avg"], st_r["exp_avg"], rtol=1e-4,
+                                   atol=1e-5 * float(st_r["exp_avg"].abs().max()))
+
+
+def test_bf16_autocast_training_step_tracks_the_fallback_model(gpu):
+    # Under autocast the kernels see the training dtypes: fp32 residual stream into the
+    # norms, bf16 gate/up into SwiGLU, bf16 query/key into RoPE, bf16 logits into the loss.
+    reference, fused = _models(gpu)
+    ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(4)).to(gpu)
+    with _no_fallback_warning():
+        loss_f, grads_f, _ = _step(fused, True, ids, eps=1e-8, autocast=True)
+    loss_r, grads_r, _ = _step(reference, False, ids, eps=1e-8, autocast=True)
+    assert abs(loss_f.item() - loss_r.item()) <= 5e-3 * abs(loss_r.item())
+    for name, g in grads_r.items():
+        cos = F.cosine_similarity(grads_f[name].flatten().double(), g.flatten().double(), dim=0)
+        assert float(cos) > 0.999, (name, float(cos))
+
+
+@contextlib.contextmanager
+def _no_fallback_warning():
+    """Fails if any fused module falls back to PyTorch (its warning says 'PyTorch fallback')."""
+
+    with warnings.catch_warnings(record=True) as records:
+        warnings.simplefilter("always")
+        yield
+    fallbacks = [str(w.message) for w in records if "PyTorch fallback" in str(w.message)]
+    assert not fallbacks, fallbacks
