@@ -69,15 +69,30 @@ def _check_param(p: Tensor) -> None:
 
 _table_cache: dict[tuple, Tensor] = {}
 _TABLE_CACHE_SIZE = 16
+# Tables used while a stream is being captured into a graph: the graph's kernels read them
+# on every replay, so they stay alive for the life of the process instead of leaving with
+# the cache's eviction.
+_captured_tables: list[Tensor] = []
 
 
 def _device_table(host_table: Tensor, device: torch.device) -> Tensor:
-    """The device copy of a record table, cached by content (tables repeat every step)."""
+    """The device copy of a record table, cached by content (tables repeat every step).
+
+    Under graph capture the table must already be cached (by an eager call on the same
+    tensors, as in the usual warm-up before a capture): building it there would need a
+    pinned host allocation and a host-to-device copy inside the graph."""
 
     key = (device, tuple(host_table.flatten().tolist()))
     cached = _table_cache.pop(key, None)
+    capturing = torch.cuda.is_current_stream_capturing()
     if cached is None:
+        if capturing:
+            raise TritonAdamWUnavailable(
+                "HIP AdamW: the tensor table is first built during graph capture; run the "
+                "same call once before capturing it.")
         cached = host_table.pin_memory().to(device, non_blocking=True)
+    if capturing:
+        _captured_tables.append(cached)
     _table_cache[key] = cached  # most recent last
     while len(_table_cache) > _TABLE_CACHE_SIZE:
         del _table_cache[next(iter(_table_cache))]
