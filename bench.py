@@ -73,14 +73,19 @@ def _cpu_info() -> tuple[int, int, str]:
 CPU_TARGET_S = 10.0  # CPU work per baseline measurement
 
 
-def _time_cpu(fn, target_s: float = CPU_TARGET_S) -> tuple[float, int]:
+def _time_cpu(fn, target_s: float = CPU_TARGET_S, setup=None) -> tuple[float, int]:
     """(median seconds per call, calls timed): one warm-up call, then calls until about
-    ``target_s`` seconds of CPU work (at least 3)."""
+    ``target_s`` seconds of CPU work (at least 3).  ``setup`` (untimed) runs before each
+    call, e.g. to restore inputs that the call modifies in place."""
 
+    if setup is not None:
+        setup()
     fn()
     times = []
     start = time.perf_counter()
     while len(times) < 3 or (time.perf_counter() - start < target_s and len(times) < 1000):
+        if setup is not None:
+            setup()
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
@@ -716,12 +721,13 @@ class AdamWClipWorkload(AdamWWorkload):
         g = self.g[:n].cpu()
         opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
 
+        p.grad = g.clone()
+
         def clip_step():
-            p.grad = g.clone()
             torch.nn.utils.clip_grad_norm_([p], 1.0)
             opt.step()
 
-        sec, calls = _time_cpu(clip_step)
+        sec, calls = _time_cpu(clip_step, setup=lambda: p.grad.copy_(g))
         return dict(
             value=36 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
             sample=f"{n:.1e} of 1.2e9 params (1/10): torch.nn.utils.clip_grad_norm_ + "
@@ -803,7 +809,43 @@ class ZeroMixedPrecisionStepWorkload(AdamWWorkload):
         return {"reference_sequence_ms_per_step": round(total / steps * 1e3, 4)}
 
     def cpu_baseline(self) -> dict:
-        return None
+        """The reference ZeRO sequence on one rank (zero.py:139-186, then the inner AdamW
+        step) in torch on the host cores, over a tenth of the parameters; the scaled
+        gradients are restored before each call, outside the timing."""
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        n = 120_000_000
+        p = torch.nn.Parameter(self.p[:n].cpu())
+        g_scaled = self.g_scaled[:n].cpu()
+        p.grad = g_scaled.clone()
+        opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+        scale = self.loss_scale
+
+        def zero_step():
+            g = p.grad
+            found = torch.zeros((), dtype=torch.int32)
+            if not torch.isfinite(g).all():
+                found.fill_(1)
+            if found.item():
+                raise RuntimeError("unexpected overflow in the synthetic gradients")
+            g.mul_(1.0 / scale)
+            sq = torch.zeros((), dtype=torch.float32)
+            sq.add_(g.detach().float().pow(2).sum())
+            coef = 1.0 / (sq.sqrt() + 1e-6)
+            if coef < 1:
+                g.mul_(coef.to(dtype=g.dtype))
+            opt.step()
+
+        sec, calls = _time_cpu(zero_step, setup=lambda: p.grad.copy_(g_scaled))
+        return dict(
+            value=36 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"{n:.1e} of 1.2e9 params (1/10): the ZeRO unscale_and_check_ + clip_grad_norm_(1.0) "
+                   f"(zero.py:139-186) + torch.optim.AdamW(foreach=False).step() on CPU, scaled gradients "
+                   f"restored untimed before each call, median of {calls} calls (~{CPU_TARGET_S:.0f} s) "
+                   f"after 1 warm-up",
+            seconds_per_call=sec, params_per_s=n / sec,
+        )
 
 
 class CopyWorkload(Workload):
