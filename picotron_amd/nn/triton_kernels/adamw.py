@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import warnings
 
+import numpy as np
 import torch
 from torch import Tensor
 from torch.optim import Optimizer
@@ -138,14 +139,18 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
     return groups, device
 
 
-def _run(optimizer: Optimizer, groups, device: torch.device, grad_scale: Tensor | None,
-         write_grad: bool) -> None:
+def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, list[Tensor]]:
+    """Host side of the fused step, touching no step counter: lazy state creation exactly as
+    torch.optim.Adam._init_group does for the non-capturable, non-fused case, and one record
+    table per distinct next step value.  Returns the launches and the parameters whose state
+    was created here (so that a skipped step can remove it again)."""
+
+    launches = []
+    created = []
     for group, params in groups:
         if not params:
             continue
         beta1, beta2 = group["betas"]
-        # Lazy state creation and step increment exactly as torch.optim.Adam._init_group /
-        # _single_tensor_adam do for the non-capturable, non-fused case.
         by_step: dict[float, list[Tensor]] = {}
         for p in params:
             state = optimizer.state[p]
@@ -153,8 +158,10 @@ def _run(optimizer: Optimizer, groups, device: torch.device, grad_scale: Tensor 
                 state["step"] = torch.tensor(0.0, dtype=torch.float32)
                 state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                 state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-            state["step"] += 1
-            by_step.setdefault(float(state["step"].item()), []).append(p)
+                created.append(p)
+            # the value `state["step"] += 1` leaves in the float32 tensor
+            step = float(np.float32(state["step"].item()) + np.float32(1.0))
+            by_step.setdefault(step, []).append(p)
         for step, ps in by_step.items():
             grads = [p.grad for p in ps]
             exp_avgs = [optimizer.state[p]["exp_avg"] for p in ps]
@@ -165,10 +172,29 @@ def _run(optimizer: Optimizer, groups, device: torch.device, grad_scale: Tensor 
             table = _device_table(host_table, device)
             hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
                          weight_decay=group["weight_decay"], step=step)
-            if grad_scale is None:
-                ops.adamw_step(table, total_blocks, **hyper)
-            else:
-                ops.adamw_step_scaled(table, total_blocks, grad_scale, write_grad=write_grad, **hyper)
+            launches.append((table, total_blocks, hyper))
+    return launches, created
+
+
+def _launch(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | None,
+            write_grad: bool) -> None:
+    """Advances every stepped parameter's step counter (as _single_tensor_adam does) and
+    launches the prepared updates."""
+
+    for _, params in groups:
+        for p in params:
+            optimizer.state[p]["step"] += 1
+    for table, total_blocks, hyper in launches:
+        if grad_scale is None:
+            ops.adamw_step(table, total_blocks, **hyper)
+        else:
+            ops.adamw_step_scaled(table, total_blocks, grad_scale, write_grad=write_grad, **hyper)
+
+
+def _run(optimizer: Optimizer, groups, device: torch.device, grad_scale: Tensor | None,
+         write_grad: bool) -> None:
+    launches, _ = _prepare(optimizer, groups, device)
+    _launch(optimizer, groups, launches, grad_scale, write_grad)
 
 
 def triton_adamw_step(optimizer: Optimizer) -> None:
@@ -247,7 +273,7 @@ def triton_unscale_and_check_(parameters, scale: float) -> bool:
     if device is None:
         return False
     table, blocks = _grad_table(grads, device)
-    inv = torch.tensor(1.0 / scale, dtype=torch.float32, device=device)
+    inv = torch.full((), 1.0 / scale, dtype=torch.float32, device=device)
     _, multiplier, found_inf = ops.grad_stats(table, blocks, inv)
     if bool(found_inf.item()):
         return True
@@ -301,17 +327,23 @@ def triton_unscale_clip_and_step(
     if device is not None and device != gdevice:
         raise _reject("gradients on several devices")
     table, blocks = _grad_table(grads, gdevice)
-    inv = torch.tensor(1.0 / scale, dtype=torch.float32, device=gdevice)
+    # a fill kernel, not a host-to-device copy (which would wait for the stream)
+    inv = torch.full((), 1.0 / scale, dtype=torch.float32, device=gdevice)
     _, multiplier, found_inf = ops.grad_stats(table, blocks, inv, max_norm, ops.CLIP_IF_BELOW_ONE)
-    if bool(found_inf.item()):
-        return True
+    # All host work of the update happens before the flag is read, so that the device idles
+    # only for the launches after it.
     owned_ids = {id(p) for p in owned}
     others = [p.grad for p in parameters if p.grad is not None and id(p) not in owned_ids]
-    if others:
-        other_table, other_blocks = _grad_table(others, gdevice)
-        ops.grad_scale(other_table, other_blocks, multiplier)
+    other = _grad_table(others, gdevice) if others else None
+    launches, created = _prepare(optimizer, groups, device) if device is not None else ([], [])
+    if bool(found_inf.item()):
+        for p in created:  # a skipped step leaves no state behind, as in the reference
+            del optimizer.state[p]
+        return True
+    if other is not None:
+        ops.grad_scale(other[0], other[1], multiplier)
     if device is not None:
-        _run(optimizer, groups, device, multiplier, True)
+        _launch(optimizer, groups, launches, multiplier, True)
     return False
 
 

@@ -113,3 +113,12 @@ def test_fused_step_skips_on_overflow_and_rescales_unowned(gpu):
     assert triton_unscale_clip_and_step(opt, 1024.0, None, parameters=owned + extra) is False
     assert torch.equal(extra[0].grad, g_extra * (1.0 / 1024.0))  # not stepped, but unscaled
     assert float(opt.state[owned[0]]["step"]) == 1.0
+    # an overflow on a later step: the existing state stays as it was, the counter included
+    moments = [(opt.state[p]["exp_avg"].clone(), opt.state[p]["exp_avg_sq"].clone()) for p in owned]
+    after_first = [p.detach().clone() for p in owned]
+    owned[1].grad[3] = float("inf")
+    assert triton_unscale_clip_and_step(opt, 1024.0, 1.0, parameters=owned + extra) is True
+    for p, b, (m, v) in zip(owned, after_first, moments):
+        assert float(opt.state[p]["step"]) == 1.0
+        assert torch.equal(p.detach(), b)
+        assert torch.equal(opt.state[p]["exp_avg"], m) and torch.equal(opt.state[p]["exp_avg_sq"], v)
