@@ -4,7 +4,8 @@
 (interleaved pairs on a ``(batch, heads, seq, head_dim)`` view).  ``RotaryEmbedding``
 keeps the reference constructor and ``forward(query, key)``; with ``use_triton_rope`` it
 rotates query and key with one fused HIP launch (autograd included) using fp32 angle
-tables cached per (sequence length, device), and warns once and falls back otherwise.
+tables cached per device (grown to the longest sequence seen), and warns once and falls
+back otherwise.
 
 The reference implements only the interleaved layout.  ``layout="rotate_half"`` (pairs
 ``(i, i + head_dim/2)``, the Llama/HF convention) is an addition; both layouts share the
@@ -100,16 +101,18 @@ class RotaryEmbedding(nn.Module):
         self.layout = layout
         self.use_triton_rope = use_triton_rope
         self._triton_fallback_warned = False
-        self._fp32_tables: dict[tuple[int, torch.device], tuple[Tensor, Tensor]] = {}
+        # One fp32 table pair per device, as long as the longest sequence seen: position p's
+        # angles do not depend on the table length, and the kernel reads rows 0..seq-1 of a
+        # longer table, so variable sequence lengths share one pair instead of one each.
+        self._fp32_tables: dict[torch.device, tuple[Tensor, Tensor]] = {}
 
     def _tables_fp32(self, sequence_length: int, device: torch.device) -> tuple[Tensor, Tensor]:
-        key = (sequence_length, device)
-        tables = self._fp32_tables.get(key)
-        if tables is None:
+        tables = self._fp32_tables.get(device)
+        if tables is None or tables[0].size(0) < sequence_length:
             tables = rotary_cos_sin(
                 sequence_length, self.head_dim, self.theta, device=device, dtype=torch.float32
             )
-            self._fp32_tables[key] = tables
+            self._fp32_tables[device] = tables
         return tables
 
     def forward(self, query: Tensor, key: Tensor) -> tuple[Tensor, Tensor]:

@@ -111,3 +111,19 @@ def test_autograd_surface_and_module(gpu, layout):
     torch.autograd.backward((rq, rk), (gq, gk))
     torch.testing.assert_close(q.grad.double(), o_rope.rotate(gq, cos, sin, layout, inverse=True), **BF16)
     torch.testing.assert_close(k.grad.double(), o_rope.rotate(gk, cos, sin, layout, inverse=True), **BF16)
+
+
+def test_module_shares_one_table_across_sequence_lengths(gpu):
+    from picotron_amd.nn import RotaryEmbedding
+
+    rope = RotaryEmbedding(64, 500_000.0, use_triton_rope=True, layout="rotate_half")
+    for seq in (48, 17, 96, 40):  # shorter lengths read a prefix of the longest table so far
+        q = _bhsd_view(2, seq, 4, 64, torch.bfloat16, gpu, seq)
+        k = _bhsd_view(2, seq, 2, 64, torch.bfloat16, gpu, seq + 1)
+        rq, rk = rope(q, k)
+        cos, sin = o_rope.tables(seq, 64, 500_000.0, device=gpu)
+        torch.testing.assert_close(rq.double(), o_rope.rotate(q, cos, sin, "rotate_half"), **BF16)
+        torch.testing.assert_close(rk.double(), o_rope.rotate(k, cos, sin, "rotate_half"), **BF16)
+    assert not rope._triton_fallback_warned
+    assert len(rope._fp32_tables) == 1
+    assert next(iter(rope._fp32_tables.values()))[0].size(0) == 96
