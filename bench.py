@@ -174,6 +174,45 @@ class RMSNormWorkload(Workload):
             if rc:
                 _lib.check("pt_rmsnorm_bwd", rc)
 
+    def extra(self, steps: int) -> dict:
+        """The forward against a plain copy of the same traffic (one 134 MB stream in, one out,
+        over the same rotating per-layer buffers), both timed per launch with HIP events on the
+        launch stream: how close the norm comes to data movement alone at this size."""
+
+        lib = _lib.lib()
+        nbytes = self.rows * self.cols * 2
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def per_launch_us(launch) -> float:
+            for i in range(self.layers):
+                launch(i)
+            pairs = []
+            for _ in range(steps):
+                for i in range(self.layers):
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    launch(i)
+                    b.record()
+                    pairs.append((a, b))
+            torch.cuda.synchronize()
+            return statistics.median(a.elapsed_time(b) * 1e3 for a, b in pairs)
+
+        def fwd(i):
+            fn, args = self._fwd[i]
+            _lib.check("pt_rmsnorm_fwd", fn(*args))
+
+        def copy(i):
+            _lib.check("pt_copy", lib.pt_copy(_p(self.x[i]), _p(self.y[i]), nbytes, stream))
+
+        fwd_us = per_launch_us(fwd)
+        copy_us = per_launch_us(copy)
+        return {
+            "forward_median_launch_us": round(fwd_us, 2),
+            "forward_gbs": round(self.fwd_bytes / fwd_us / 1e3, 1),
+            "same_size_copy_median_launch_us": round(copy_us, 2),
+            "same_size_copy_gbs": round(2 * nbytes / copy_us / 1e3, 1),
+        }
+
     def cpu_baseline(self) -> dict:
         from oracle import rmsnorm as o_rms
 
