@@ -239,6 +239,22 @@ int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_
                          double beta1, double beta2, double eps, double weight_decay, double step,
                          const float* grad_scale, int write_grad, void* stream);
 
+/* The step of a torch.optim.AdamW(..., capturable=True), which is what the reference's
+ * fallback (optimizer.step(), src/picotron/nn/triton_kernels/adamw.py:47) runs for such an
+ * optimizer: each parameter's step count is an fp32 scalar in device memory, advanced by the
+ * caller before the update (torch: state["step"] += 1 on the device).  `step_table` is a
+ * DEVICE array of n_tensors int64 addresses, the step of each `table` record in record
+ * order.  Every workgroup reads its tensor's step t and forms, in fp32,
+ * step_size = lr / (1 - beta1^t) and bias_correction2_sqrt = sqrt(1 - beta2^t); the update
+ * is otherwise pt_adamw_step's.  With grad_scale non-NULL the gradients are scaled (and
+ * written back when write_grad != 0) as in pt_adamw_step_scaled.  No argument depends on
+ * the step's value, so the launch can be captured in a HIP graph and replayed as the step
+ * advances. */
+int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                              const int64_t* step_table, double lr, double beta1, double beta2,
+                              double eps, double weight_decay, const float* grad_scale,
+                              int write_grad, void* stream);
+
 /* Mixed-precision / ZeRO gradient handling before the step
  * (src/picotron/parallel/zero.py:139-163 unscale_and_check_: a finite check of every
  * gradient, one host sync per parameter, then g *= 1/scale; :165-186 clip_grad_norm_:

@@ -103,6 +103,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int64, c_double, c_double, c_double, c_double, c_double, c_double,
          c_void_p, c_int, c_void_p],
     ),
+    "pt_adamw_step_device_step": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_double, c_double, c_double, c_double, c_double,
+         c_void_p, c_int, c_void_p],
+    ),
     "pt_grad_stats_workspace_bytes": (c_size_t, [c_int64]),
     "pt_grad_stats": (
         c_int,

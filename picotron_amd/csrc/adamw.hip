@@ -73,16 +73,35 @@ __device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v,
   p = p + s.neg_step * __fdiv_rn(m, denom);
 }
 
+// Step counts on the device (torch's capturable AdamW keeps each parameter's step as an
+// fp32 scalar next to it, advanced by the caller before the update): `steps[i]` is the
+// address of table row i's step.  Each workgroup reads its tensor's step and forms the bias
+// corrections in fp32, step_size = lr / (1 - beta1^t) and bc2_sqrt = sqrt(1 - beta2^t), in
+// place of the host-computed ones; nothing in the launch depends on the step's value, so a
+// captured graph replays correctly as the step advances.
+struct DevStep {
+  const int64_t* steps;
+  float lr, beta1, beta2;
+};
+
+__device__ __forceinline__ void device_step_scalars(AdamScalars& s, const DevStep& d, int64_t row) {
+  const float t = *as_global<const float>(d.steps[row]);
+  s.neg_step = -__fdiv_rn(d.lr, 1.0f - powf(d.beta1, t));
+  s.bc2_sqrt = __fsqrt_rn(1.0f - powf(d.beta2, t));
+}
+
 // SCALED: the gradient is multiplied by *grad_scale as it is read (torch's clipping
 // multiplies the stored gradient, g = g * coef, before the step reads it), and written back
-// when write_grad != 0.
-template <bool SCALED>
+// when write_grad != 0.  DEVSTEP: bias corrections from the device step counts (DevStep).
+template <bool SCALED, bool DEVSTEP>
 __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restrict__ table,
                                                          int64_t ntensors, AdamScalars s,
                                                          const float* __restrict__ grad_scale,
-                                                         int write_grad) {
+                                                         int write_grad, DevStep ds) {
   const int64_t blk = blockIdx.x;
-  const AdamRec r = table[find_tensor(table, ntensors, blk)];
+  const int64_t row = find_tensor(table, ntensors, blk);
+  const AdamRec r = table[row];
+  if constexpr (DEVSTEP) device_step_scalars(s, ds, row);
   const float gs = SCALED ? *grad_scale : 1.0f;
   const int64_t start = (blk - r.first_block) * kBlockElems;
   const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
@@ -345,10 +364,10 @@ int pt_adamw_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
   if (rc == -1) return ok();
   if (rc != PT_OK) return rc;
   if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step: step must be >= 1");
-  hipLaunchKernelGGL(adamw_kernel<false>, dim3(static_cast<unsigned>(total_blocks)),
+  hipLaunchKernelGGL((adamw_kernel<false, false>), dim3(static_cast<unsigned>(total_blocks)),
                      dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
                      n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step),
-                     static_cast<const float*>(nullptr), 0);
+                     static_cast<const float*>(nullptr), 0, DevStep{});
   return check_launch("pt_adamw_step");
 }
 
@@ -360,11 +379,37 @@ int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_
   if (rc != PT_OK) return rc;
   if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step_scaled: step must be >= 1");
   if (!grad_scale) return fail(PT_EINVAL, "pt_adamw_step_scaled: null grad_scale");
-  hipLaunchKernelGGL(adamw_kernel<true>, dim3(static_cast<unsigned>(total_blocks)),
+  hipLaunchKernelGGL((adamw_kernel<true, false>), dim3(static_cast<unsigned>(total_blocks)),
                      dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
                      n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step), grad_scale,
-                     write_grad);
+                     write_grad, DevStep{});
   return check_launch("pt_adamw_step_scaled");
+}
+
+int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
+                              const int64_t* step_table, double lr, double beta1, double beta2,
+                              double eps, double weight_decay, const float* grad_scale,
+                              int write_grad, void* stream) {
+  const int rc = check_table("pt_adamw_step_device_step", table, n_tensors, total_blocks);
+  if (rc == -1) return ok();
+  if (rc != PT_OK) return rc;
+  if (!step_table || (reinterpret_cast<uintptr_t>(step_table) & 7u) != 0)
+    return fail(PT_EINVAL, "pt_adamw_step_device_step: null or misaligned step table");
+  // decay, lerp weight, beta2 and eps as for a host step; the bias corrections per workgroup
+  const AdamScalars s = host_scalars(lr, beta1, beta2, eps, weight_decay, 1.0);
+  const DevStep d{step_table, static_cast<float>(lr), static_cast<float>(beta1),
+                  static_cast<float>(beta2)};
+  hipStream_t st = as_stream(stream);
+  const AdamRec* t = reinterpret_cast<const AdamRec*>(table);
+  if (grad_scale) {
+    hipLaunchKernelGGL((adamw_kernel<true, true>), dim3(static_cast<unsigned>(total_blocks)),
+                       dim3(kThreads), 0, st, t, n_tensors, s, grad_scale, write_grad, d);
+  } else {
+    hipLaunchKernelGGL((adamw_kernel<false, true>), dim3(static_cast<unsigned>(total_blocks)),
+                       dim3(kThreads), 0, st, t, n_tensors, s, static_cast<const float*>(nullptr),
+                       0, d);
+  }
+  return check_launch("pt_adamw_step_device_step");
 }
 
 // One fp32 partial (and one int flag) per workgroup of the statistics walk, which has at

@@ -11,9 +11,12 @@ falling back is always possible.  Hyperparameters are read from ``param_groups``
 call (the train loop rewrites ``lr`` each step, train_loop.py:127,328-335).
 
 Supported: fp32 dense parameters and gradients on a gfx950 device, ``amsgrad=False``,
-``maximize=False``, ``capturable=False``, ``differentiable=False``, float ``lr``.  Anything
-else raises :class:`TritonAdamWUnavailable` (a ``RuntimeError`` whose message says "not
-implemented"), and the fallback runs torch's own step.
+``maximize=False``, ``differentiable=False``, float ``lr``.  Anything else raises
+:class:`TritonAdamWUnavailable` (a ``RuntimeError`` whose message says "not implemented"),
+and the fallback runs torch's own step.  With ``capturable=True`` the step counts stay fp32
+scalars on the device, advanced there, and the kernel reads them: no host value depends on
+the step, so a whole training step (forward, backward, clipping, this update) can be
+captured in a HIP graph and replayed.
 
 ``triton_clip_grad_norm_and_step(optimizer, max_norm)`` fuses the gradient clipping the
 train loop runs right before the step (reference src/picotron/training/train_loop.py:163-168
@@ -43,7 +46,7 @@ def _reject(reason: str) -> TritonAdamWUnavailable:
 
 
 def _check_group(group: dict) -> None:
-    for flag in ("amsgrad", "maximize", "capturable", "differentiable"):
+    for flag in ("amsgrad", "maximize", "differentiable"):
         if group.get(flag, False):
             raise _reject(f"{flag}=True")
     if group.get("fused"):
@@ -117,6 +120,11 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
                 device = p.device
             elif p.device != device:
                 raise _reject("parameters on several devices")
+            if group.get("capturable", False) and len(optimizer.state[p]) != 0:
+                step = optimizer.state[p]["step"]
+                if (not isinstance(step, Tensor) or step.device != p.device
+                        or step.dtype != torch.float32 or step.numel() != 1):
+                    raise _reject("capturable steps that are not fp32 scalars on the parameter's device")
         groups.append((group, params))
     if device is None:
         return groups, None
@@ -141,9 +149,11 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
 
 def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, list[Tensor]]:
     """Host side of the fused step, touching no step counter: lazy state creation exactly as
-    torch.optim.Adam._init_group does for the non-capturable, non-fused case, and one record
-    table per distinct next step value.  Returns the launches and the parameters whose state
-    was created here (so that a skipped step can remove it again)."""
+    torch.optim.Adam._init_group does for the non-fused case (a CPU fp32 step, or for a
+    capturable group an fp32 step on the parameter's device), and the record tables: one per
+    distinct next step value, or for a capturable group one with the table of its device
+    steps.  Returns the launches and the parameters whose state was created here (so that a
+    skipped step can remove it again)."""
 
     launches = []
     created = []
@@ -151,18 +161,30 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
         if not params:
             continue
         beta1, beta2 = group["betas"]
-        by_step: dict[float, list[Tensor]] = {}
+        capturable = bool(group.get("capturable", False))
         for p in params:
             state = optimizer.state[p]
             if len(state) == 0:
-                state["step"] = torch.tensor(0.0, dtype=torch.float32)
+                if capturable:
+                    state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
+                else:
+                    state["step"] = torch.tensor(0.0, dtype=torch.float32)
                 state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                 state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                 created.append(p)
-            # the value `state["step"] += 1` leaves in the float32 tensor
-            step = float(np.float32(state["step"].item()) + np.float32(1.0))
-            by_step.setdefault(step, []).append(p)
-        for step, ps in by_step.items():
+        hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
+                     weight_decay=group["weight_decay"])
+        if capturable:
+            # the step values stay on the device: no host read, one launch for the group
+            buckets = [(None, params)]
+        else:
+            by_step: dict[float, list[Tensor]] = {}
+            for p in params:
+                # the value `state["step"] += 1` leaves in the float32 tensor
+                step = float(np.float32(optimizer.state[p]["step"].item()) + np.float32(1.0))
+                by_step.setdefault(step, []).append(p)
+            buckets = list(by_step.items())
+        for step, ps in buckets:
             grads = [p.grad for p in ps]
             exp_avgs = [optimizer.state[p]["exp_avg"] for p in ps]
             exp_avg_sqs = [optimizer.state[p]["exp_avg_sq"] for p in ps]
@@ -170,22 +192,33 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
             if total_blocks == 0:
                 continue
             table = _device_table(host_table, device)
-            hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
-                         weight_decay=group["weight_decay"], step=step)
-            launches.append((table, total_blocks, hyper))
+            if step is None:
+                steps = _device_table(
+                    ops.adamw_step_table(ps, [optimizer.state[p]["step"] for p in ps]), device)
+                launches.append((table, total_blocks, steps, hyper))
+            else:
+                launches.append((table, total_blocks, None, dict(hyper, step=step)))
     return launches, created
 
 
 def _launch(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | None,
             write_grad: bool) -> None:
-    """Advances every stepped parameter's step counter (as _single_tensor_adam does) and
-    launches the prepared updates."""
+    """Advances every stepped parameter's step counter (as torch's AdamW does: on the host,
+    or for a capturable group on the device) and launches the prepared updates."""
 
-    for _, params in groups:
-        for p in params:
-            optimizer.state[p]["step"] += 1
-    for table, total_blocks, hyper in launches:
-        if grad_scale is None:
+    for group, params in groups:
+        if not params:
+            continue
+        if group.get("capturable", False):
+            torch._foreach_add_([optimizer.state[p]["step"] for p in params], 1.0)
+        else:
+            for p in params:
+                optimizer.state[p]["step"] += 1
+    for table, total_blocks, steps, hyper in launches:
+        if steps is not None:
+            ops.adamw_step_device_step(table, total_blocks, steps, grad_scale=grad_scale,
+                                       write_grad=write_grad, **hyper)
+        elif grad_scale is None:
             ops.adamw_step(table, total_blocks, **hyper)
         else:
             ops.adamw_step_scaled(table, total_blocks, grad_scale, write_grad=write_grad, **hyper)

@@ -511,6 +511,46 @@ def adamw_step_scaled(
     )
 
 
+def adamw_step_table(params: list[Tensor], steps: list[Tensor]) -> Tensor:
+    """Host int64 [n] addresses of the fp32 device step of each parameter, in the row order
+    of :func:`adamw_table` (which skips empty parameters)."""
+
+    addrs = [s.data_ptr() for p, s in zip(params, steps) if p.numel() > 0]
+    return torch.tensor(addrs, dtype=torch.int64) if addrs else torch.empty(0, dtype=torch.int64)
+
+
+def adamw_step_device_step(
+    table_device: Tensor,
+    total_blocks: int,
+    step_table_device: Tensor,
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    grad_scale: Tensor | None = None,
+    write_grad: bool = False,
+) -> None:
+    """:func:`adamw_step` (or :func:`adamw_step_scaled` with ``grad_scale``) for a capturable
+    optimizer: the step counts are fp32 device scalars, already advanced, whose addresses
+    ``step_table_device`` lists in table row order."""
+
+    device = _check_cuda(table_device, step_table_device)
+    if step_table_device.dtype != torch.int64 or step_table_device.numel() != table_device.size(0):
+        raise ValueError("the step table needs one int64 address per table row")
+    if grad_scale is not None:
+        _check_cuda(grad_scale)
+        if grad_scale.dtype != torch.float32 or grad_scale.numel() != 1:
+            raise ValueError("grad_scale must be one fp32 element")
+    _lib.call(
+        "pt_adamw_step_device_step",
+        table_device.data_ptr(), table_device.size(0), int(total_blocks), step_table_device.data_ptr(),
+        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), _ptr(grad_scale),
+        int(write_grad), _stream(device),
+    )
+
+
 def clip_grad_norm(table_device: Tensor, total_blocks: int, max_norm: float) -> tuple[Tensor, Tensor]:
     """(total_norm, clip_coef) fp32 device scalars over the gradients of a table built by
     :func:`adamw_table`: torch.nn.utils.clip_grad_norm_'s norm and clamped coefficient."""
