@@ -1,8 +1,11 @@
 // Library-wide C ABI: version, per-thread error message, device gate, and the
 // 128-bit streaming copy used as the achievable-bandwidth reference.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <map>
 #include <string>
+#include <utility>
 
 #include "pt_common.hpp"
 
@@ -14,6 +17,31 @@ thread_local std::string g_last_error;
 constexpr int kMaxDevices = 64;
 int g_cus[kMaxDevices];
 std::once_flag g_cus_once[kMaxDevices];
+size_t g_lds[kMaxDevices];
+std::once_flag g_lds_once[kMaxDevices];
+std::mutex g_lds_mutex;
+std::map<std::pair<int, const void*>, size_t> g_lds_raised;  // (device, kernel) -> bytes allowed
+
+int current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  return dev;
+}
+
+size_t lds_per_cu() {
+  const int dev = current_device();
+  if (dev < 0) return 163840;
+  std::call_once(g_lds_once[dev], [dev] {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
+            hipSuccess ||
+        n <= 0) {
+      n = 163840;
+    }
+    g_lds[dev] = static_cast<size_t>(n);
+  });
+  return g_lds[dev];
+}
 }  // namespace
 
 int fail(int code, const std::string& msg) {
@@ -46,6 +74,38 @@ int num_cus() {
     g_cus[dev] = n;
   });
   return g_cus[dev];
+}
+
+size_t occupancy_lds(int per_cu, size_t static_lds) {
+  if (per_cu <= 0) return 0;
+  // Each workgroup takes a 1/per_cu share of the CU's LDS, less a margin that keeps the
+  // share above 1/(per_cu + 1) of it (true for per_cu <= 12), so exactly per_cu fit.
+  const size_t share = lds_per_cu() / static_cast<size_t>(per_cu) - 1024;
+  return share > static_lds ? share - static_lds : 0;
+}
+
+int allow_dynamic_lds(const void* kernel, size_t bytes) {
+  if (bytes <= 65536) return PT_OK;
+  const int dev = current_device();
+  std::lock_guard<std::mutex> lock(g_lds_mutex);
+  size_t& allowed = g_lds_raised[{dev, kernel}];
+  if (allowed >= bytes) return PT_OK;
+  const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           static_cast<int>(bytes));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // a refused attribute must not surface as the next launch's error
+    return fail(PT_ELAUNCH, std::string("dynamic LDS limit: ") + hipGetErrorString(e));
+  }
+  allowed = bytes;
+  return PT_OK;
+}
+
+int64_t env_int(const char* name, int64_t fallback) {
+  const char* v = std::getenv(name);
+  if (v == nullptr || *v == '\0') return fallback;
+  char* end = nullptr;
+  const long long x = std::strtoll(v, &end, 10);
+  return (end != v && x >= 0) ? static_cast<int64_t>(x) : fallback;
 }
 
 // Grid-stride 16-byte copy; UNROLL independent vectors in flight per thread.

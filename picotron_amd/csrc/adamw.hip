@@ -318,6 +318,27 @@ __global__ __launch_bounds__(kThreads) void grad_scale_kernel(const AdamRec* __r
   }
 }
 
+// Resident step workgroups per CU (each thread keeps four 16-byte loads in flight): at
+// 1.2e9 parameters the plain step measured 5.67-5.75 ms with the full 8 and 5.22-5.62 ms
+// at 3; with the clip fused, 7.50-7.52 ms against 7.10-7.11 ms.  PT_ADAMW_BLOCKS_PER_CU
+// overrides it (0: no limit).
+int step_occupancy() {
+  static const int v = static_cast<int>(env_int("PT_ADAMW_BLOCKS_PER_CU", 3));
+  return v;
+}
+
+template <bool SCALED, bool DEVSTEP>
+int launch_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks, AdamScalars s,
+                const float* grad_scale, int write_grad, DevStep d, void* stream, const char* fn) {
+  const auto kernel = adamw_kernel<SCALED, DEVSTEP>;
+  size_t lds = occupancy_lds(step_occupancy(), 0);
+  if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total_blocks)), dim3(kThreads), lds,
+                     as_stream(stream), reinterpret_cast<const AdamRec*>(table), n_tensors, s,
+                     grad_scale, write_grad, d);
+  return check_launch(fn);
+}
+
 AdamScalars host_scalars(double lr, double beta1, double beta2, double eps, double weight_decay,
                          double step) {
   // torch.optim.adamw._single_tensor_adamw, in Python floats (double):
@@ -364,11 +385,9 @@ int pt_adamw_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
   if (rc == -1) return ok();
   if (rc != PT_OK) return rc;
   if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step: step must be >= 1");
-  hipLaunchKernelGGL((adamw_kernel<false, false>), dim3(static_cast<unsigned>(total_blocks)),
-                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
-                     n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step),
-                     static_cast<const float*>(nullptr), 0, DevStep{});
-  return check_launch("pt_adamw_step");
+  return launch_step<false, false>(table, n_tensors, total_blocks,
+                                   host_scalars(lr, beta1, beta2, eps, weight_decay, step), nullptr,
+                                   0, DevStep{}, stream, "pt_adamw_step");
 }
 
 int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_blocks, double lr,
@@ -379,11 +398,9 @@ int pt_adamw_step_scaled(const int64_t* table, int64_t n_tensors, int64_t total_
   if (rc != PT_OK) return rc;
   if (!(step >= 1.0)) return fail(PT_EINVAL, "pt_adamw_step_scaled: step must be >= 1");
   if (!grad_scale) return fail(PT_EINVAL, "pt_adamw_step_scaled: null grad_scale");
-  hipLaunchKernelGGL((adamw_kernel<true, false>), dim3(static_cast<unsigned>(total_blocks)),
-                     dim3(kThreads), 0, as_stream(stream), reinterpret_cast<const AdamRec*>(table),
-                     n_tensors, host_scalars(lr, beta1, beta2, eps, weight_decay, step), grad_scale,
-                     write_grad, DevStep{});
-  return check_launch("pt_adamw_step_scaled");
+  return launch_step<true, false>(table, n_tensors, total_blocks,
+                                  host_scalars(lr, beta1, beta2, eps, weight_decay, step),
+                                  grad_scale, write_grad, DevStep{}, stream, "pt_adamw_step_scaled");
 }
 
 int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks,
@@ -399,17 +416,11 @@ int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t t
   const AdamScalars s = host_scalars(lr, beta1, beta2, eps, weight_decay, 1.0);
   const DevStep d{step_table, static_cast<float>(lr), static_cast<float>(beta1),
                   static_cast<float>(beta2)};
-  hipStream_t st = as_stream(stream);
-  const AdamRec* t = reinterpret_cast<const AdamRec*>(table);
-  if (grad_scale) {
-    hipLaunchKernelGGL((adamw_kernel<true, true>), dim3(static_cast<unsigned>(total_blocks)),
-                       dim3(kThreads), 0, st, t, n_tensors, s, grad_scale, write_grad, d);
-  } else {
-    hipLaunchKernelGGL((adamw_kernel<false, true>), dim3(static_cast<unsigned>(total_blocks)),
-                       dim3(kThreads), 0, st, t, n_tensors, s, static_cast<const float*>(nullptr),
-                       0, d);
-  }
-  return check_launch("pt_adamw_step_device_step");
+  if (grad_scale)
+    return launch_step<true, true>(table, n_tensors, total_blocks, s, grad_scale, write_grad, d,
+                                   stream, "pt_adamw_step_device_step");
+  return launch_step<false, true>(table, n_tensors, total_blocks, s, nullptr, 0, d, stream,
+                                  "pt_adamw_step_device_step");
 }
 
 // One fp32 partial (and one int flag) per workgroup of the statistics walk, which has at

@@ -676,11 +676,26 @@ struct CeRows {
   int64_t tos, tis, ignore_index;
 };
 
+// Resident row workgroups per CU (0: no limit); PT_CE_OCCUPANCY overrides it.
+int rows_occupancy() {
+  static const int v = static_cast<int>(env_int("PT_CE_OCCUPANCY", 0));
+  return v;
+}
+
+// Dynamic LDS bytes that apply the row-kernel occupancy limit to `kernel` (0 when there is
+// none, or when the runtime refuses the allocation).
+size_t rows_lds(const void* kernel) {
+  const size_t lds = occupancy_lds(rows_occupancy(), 0);
+  return allow_dynamic_lds(kernel, lds) == PT_OK ? lds : 0;
+}
+
 template <typename T, int VPT>
 void launch_rows(const CeRows& d, int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
-  hipLaunchKernelGGL((ce_rows_kernel<T, VPT>), dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                     0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is,
-                     d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
+  const auto kernel = ce_rows_kernel<T, VPT>;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
+                     rows_lds(reinterpret_cast<const void*>(kernel)), st, static_cast<T*>(d.logits),
+                     d.inner, d.valid_inner, d.os, d.is, d.vocab, d.targets, d.tos, d.tis,
+                     d.ignore_index, write_grad, ws);
 }
 
 // Register-resident rows for up to 16 vectors per thread (131072 fp16/bf16 or 65536 fp32
@@ -709,10 +724,12 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
     // Rows whose body fits in 1, 2, 4 or 8 kept chunks are read once; longer rows keep
     // kKeepChunks and stream the rest twice.  Fewer kept chunks leave room for two
     // workgroups per CU.
-#define PT_CE_BATCHED(K)                                                                       \
-  hipLaunchKernelGGL((ce_rows_batched_kernel<T, K>), dim3(static_cast<unsigned>(rows)),       \
-                     dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner, \
-                     d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws)
+#define PT_CE_BATCHED(K)                                                                        \
+  hipLaunchKernelGGL((ce_rows_batched_kernel<T, K>), dim3(static_cast<unsigned>(rows)),        \
+                     dim3(kThreads),                                                           \
+                     rows_lds(reinterpret_cast<const void*>(ce_rows_batched_kernel<T, K>)), st, \
+                     static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is, d.vocab,     \
+                     d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws)
     if (per_thread <= 1) {
       PT_CE_BATCHED(1);
     } else if (per_thread <= 2) {

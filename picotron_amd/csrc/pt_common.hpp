@@ -25,6 +25,24 @@ int ok();
 int check_launch(const char* what);
 // Number of compute units of the current device (cached per device).
 int num_cus();
+// Resident-workgroup limit for streaming kernels.  A kernel that keeps several 16-byte loads
+// in flight per thread moves more bytes per second with fewer workgroups per CU: the DRAM
+// then sees fewer interleaved streams.  Measured on MI355X with one-shot grids of 256-thread
+// workgroups: 4 fp32 streams read and 3 written, 5873 GB/s at the full 8 workgroups per CU
+// against 6419 at 3; 3 read and 2 written, 5963 against 6374 at 2.  A plain copy with one
+// load per thread is fastest uncapped.  The limit is a dynamic LDS allocation that the
+// kernel never touches.
+// Bytes of dynamic LDS that keep at most `per_cu` workgroups (each also holding
+// `static_lds` bytes of its own) resident on one CU of the current device; 0 for
+// per_cu <= 0 (no limit).
+size_t occupancy_lds(int per_cu, size_t static_lds);
+// Lets `kernel` launch with `bytes` of dynamic LDS (raises the 64 KB default once per
+// kernel and device when needed); returns PT_OK, or PT_ELAUNCH when the runtime refuses
+// (callers then launch without the limit: same results, default occupancy).
+int allow_dynamic_lds(const void* kernel, size_t bytes);
+// A non-negative integer from the environment variable `name`, or `fallback` when it is
+// unset or not a number (callers read it once, into a static, for tuning experiments).
+int64_t env_int(const char* name, int64_t fallback);
 // Fills `count` elements of 4 or 2 bytes at device address `p` with `value` using a kernel
 // (not hipMemsetAsync, so the call is safe inside captured graphs).
 int fill(void* p, int64_t count, int elem_bytes, unsigned value, hipStream_t st);

@@ -577,6 +577,8 @@ struct Tuning {
   int bwd_vpl_cap = 0;  // 0: by row length (bwd_vpl_cap_for)
   int64_t fwd_blocks_per_cu = 0;  // 0: no cap (one row per row slot)
   int64_t bwd_partials = 512;
+  int fwd_occupancy = 0;  // resident forward workgroups per CU (0: no limit)
+  int bwd_occupancy = 0;  // resident backward workgroups per CU (0: no limit)
 };
 
 // Backward vectors per lane: one for rows of at most 256 16-byte vectors (bf16 hidden
@@ -602,6 +604,8 @@ inline const Tuning& tuning() {
     d.bwd_vpl_cap = static_cast<int>(env_positive("PT_RMSNORM_BWD_VPL_CAP", d.bwd_vpl_cap));
     d.fwd_blocks_per_cu = env_positive("PT_RMSNORM_FWD_BLOCKS_PER_CU", d.fwd_blocks_per_cu);
     d.bwd_partials = env_positive("PT_RMSNORM_BWD_PARTIALS", d.bwd_partials);
+    d.fwd_occupancy = static_cast<int>(env_int("PT_RMSNORM_FWD_OCCUPANCY", d.fwd_occupancy));
+    d.bwd_occupancy = static_cast<int>(env_int("PT_RMSNORM_BWD_OCCUPANCY", d.bwd_occupancy));
     return d;
   }();
   return t;
@@ -746,11 +750,13 @@ struct FwdLaunch {
   void go(int iters) const {
     constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
     const ResidualIn<T> rin{static_cast<const T*>(a.res), a.res_s, static_cast<T*>(a.h), a.h_s};
-    hipLaunchKernelGGL(
-        (rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, PERSIST, ADD>),
-        dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), 0, a.st,
-        static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys, a.rstd, a.rows,
-        a.cols, a.eps, iters, rin);
+    const auto kernel =
+        rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, PERSIST, ADD>;
+    size_t lds = occupancy_lds(tuning().fwd_occupancy, 0);
+    if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
+                       static_cast<const T*>(a.x), a.xs, a.w, a.wdt, static_cast<T*>(a.y), a.ys,
+                       a.rstd, a.rows, a.cols, a.eps, iters, rin);
   }
   template <int VPL, int WPR>
   void run() const {
@@ -777,22 +783,26 @@ struct BwdLaunch {
   void run() const {
     constexpr int WAVES = WPR > kBwdWaves ? WPR : kBwdWaves;
     constexpr int RPB = WAVES / WPR;
-    const size_t lds =
+    const size_t need =
         (RPB > 1 && a.partial != nullptr) ? static_cast<size_t>(a.cols) * sizeof(float) : 0;
+    const size_t share = occupancy_lds(tuning().bwd_occupancy, 0);
+    size_t lds = share > need ? share : need;
     const ResidualGrad<T> rg{static_cast<const T*>(a.dh_in), a.dh_in_s};
     const int iters = row_iters(a.rows, a.blocks, RPB);
     if (a.dh_in != nullptr) {
-      hipLaunchKernelGGL(
-          (rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>),
-          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
-          static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs, a.w, a.wdt,
-          a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows, a.cols, iters, rg);
+      const auto kernel = rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>;
+      if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = need;
+      hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds,
+                         a.st, static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x),
+                         a.xs, a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
+                         a.cols, iters, rg);
     } else {
-      hipLaunchKernelGGL(
-          (rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>),
-          dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
-          static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs, a.w, a.wdt,
-          a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows, a.cols, iters, rg);
+      const auto kernel = rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>;
+      if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = need;
+      hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds,
+                         a.st, static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x),
+                         a.xs, a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
+                         a.cols, iters, rg);
     }
   }
 };

@@ -229,6 +229,21 @@ bool parse(const void* x, void* y, const int64_t* d, int64_t head_dim, int64_t t
 
 constexpr int64_t kNontemporalBytes = int64_t{64} << 20;
 
+// Resident workgroups per CU (0: no limit); PT_ROPE_OCCUPANCY overrides it.
+int rope_occupancy() {
+  static const int v = static_cast<int>(env_int("PT_ROPE_OCCUPANCY", 0));
+  return v;
+}
+
+template <typename K>
+void launch_limited(K kernel, unsigned grid, hipStream_t st, const RopeTensor& t0,
+                    const RopeTensor& t1, int head_dim, const float* c, const float* s,
+                    float sign) {
+  size_t lds = occupancy_lds(rope_occupancy(), 0);
+  if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, st, t0, t1, head_dim, c, s, sign);
+}
+
 template <typename T, int LAYOUT, bool ALIGNED>
 void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const float* s,
             float sign, hipStream_t st) {
@@ -245,11 +260,11 @@ void launch(RopeTensor& t0, RopeTensor& t1, int head_dim, const float* c, const 
   // nontemporal loads and stores.
   const int64_t bytes = (t0.rows + t1.rows) * head_dim * static_cast<int64_t>(sizeof(T));
   if (bytes > kNontemporalBytes) {
-    hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED, true>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+    launch_limited(rope_kernel<T, LAYOUT, ALIGNED, true>, static_cast<unsigned>(blocks), st, t0,
+                   t1, head_dim, c, s, sign);
   } else {
-    hipLaunchKernelGGL((rope_kernel<T, LAYOUT, ALIGNED, false>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(256), 0, st, t0, t1, head_dim, c, s, sign);
+    launch_limited(rope_kernel<T, LAYOUT, ALIGNED, false>, static_cast<unsigned>(blocks), st, t0,
+                   t1, head_dim, c, s, sign);
   }
 }
 

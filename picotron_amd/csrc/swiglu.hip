@@ -131,10 +131,34 @@ __global__ __launch_bounds__(256) void swiglu_bwd_elem_kernel(const T* __restric
   }
 }
 
+// Vectors per stream per thread.  The backward (3 streams read, 2 written) keeps two in
+// flight and runs 2 workgroups per CU: [16384, 14336] bf16 366-367 us, against 383 us with
+// four vectors at full occupancy and 395-399 us with two at full occupancy.  The forward
+// is fastest with four vectors and no limit (212-216 us at every limit tried).
 constexpr int kFwdUnroll = 4;
-constexpr int kBwdUnroll = 4;
+constexpr int kBwdUnroll = 2;
 // Streams above this many bytes bypass cache retention (nontemporal).
 constexpr int64_t kNontemporalBytes = int64_t{64} << 20;
+
+// Resident workgroups per CU of the vector kernels (0: no limit); PT_SWIGLU_FWD_OCCUPANCY
+// and PT_SWIGLU_BWD_OCCUPANCY override them.
+int fwd_occupancy() {
+  static const int v = static_cast<int>(env_int("PT_SWIGLU_FWD_OCCUPANCY", 0));
+  return v;
+}
+int bwd_occupancy() {
+  static const int v = static_cast<int>(env_int("PT_SWIGLU_BWD_OCCUPANCY", 2));
+  return v;
+}
+
+// Launches `kernel` with the dynamic LDS that limits it to `per_cu` resident workgroups
+// per CU (or without a limit when the runtime refuses the allocation).
+template <typename K, typename... Args>
+void launch_limited(K kernel, int per_cu, unsigned grid, hipStream_t st, Args... args) {
+  size_t lds = occupancy_lds(per_cu, 0);
+  if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, st, args...);
+}
 
 unsigned grid_for(int64_t items, int per_block) {
   int64_t b = (items + per_block - 1) / per_block;
@@ -156,11 +180,11 @@ void launch_fwd(const void* g, const void* u, void* o, int64_t n, hipStream_t st
     const bool nt = n * static_cast<int64_t>(sizeof(T)) > kNontemporalBytes;
     const unsigned grid = grid_for(nvec, 256 * kFwdUnroll);
     if (nt) {
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, kFwdUnroll, true>), dim3(grid), dim3(256), 0, st,
-                         gp, up, op, nvec);
+      launch_limited(swiglu_fwd_kernel<T, kFwdUnroll, true>, fwd_occupancy(), grid, st, gp, up, op,
+                     nvec);
     } else {
-      hipLaunchKernelGGL((swiglu_fwd_kernel<T, kFwdUnroll, false>), dim3(grid), dim3(256), 0, st,
-                         gp, up, op, nvec);
+      launch_limited(swiglu_fwd_kernel<T, kFwdUnroll, false>, fwd_occupancy(), grid, st, gp, up,
+                     op, nvec);
     }
   }
   const int64_t start = nvec * V;
@@ -186,11 +210,11 @@ void launch_bwd(const void* dy, const void* g, const void* u, void* dg, void* du
     const bool nt = n * static_cast<int64_t>(sizeof(T)) > kNontemporalBytes;
     const unsigned grid = grid_for(nvec, 256 * kBwdUnroll);
     if (nt) {
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, kBwdUnroll, true>), dim3(grid), dim3(256), 0, st,
-                         dyp, gp, up, dgp, dup, nvec);
+      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, true>, bwd_occupancy(), grid, st, dyp, gp, up,
+                     dgp, dup, nvec);
     } else {
-      hipLaunchKernelGGL((swiglu_bwd_kernel<T, kBwdUnroll, false>), dim3(grid), dim3(256), 0, st,
-                         dyp, gp, up, dgp, dup, nvec);
+      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, false>, bwd_occupancy(), grid, st, dyp, gp,
+                     up, dgp, dup, nvec);
     }
   }
   const int64_t start = nvec * V;
