@@ -295,6 +295,27 @@ def test_shifted_autograd_surface(gpu):
     _grad_close(x.grad, ref_grad, n_valid, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("vocab", [3, 7, 8, 9, 1001, 50257])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_scale_grad_is_the_elementwise_product(gpu, dtype, vocab, offset):
+    # rows split into head / 16-byte body / tail at every alignment (row starts shifted by a
+    # one-element view offset): each kept element becomes (x * scale) rounded once, bit for
+    # bit; ignored rows are left alone
+    rows = 11
+    base = randn((rows, vocab + offset), dtype, gpu, vocab + offset)
+    buf = base[:, offset:]
+    targets = torch.randint(0, vocab, (rows,), device=gpu)
+    targets[[2, 7]] = -100
+    before = buf.clone()
+    outside = base[:, :offset].clone()
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu))
+    kept = (targets != -100).unsqueeze(1)
+    want = torch.where(kept, (before.float() * 0.37).to(dtype), before)
+    assert torch.equal(buf, want)
+    assert torch.equal(base[:, :offset], outside)  # nothing outside the view is written
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("vocab", [512, 1001, 131072])
 def test_scale_grad(gpu, dtype, vocab):
