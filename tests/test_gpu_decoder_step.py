@@ -137,6 +137,32 @@ def test_bf16_autocast_training_step_tracks_the_fallback_model(gpu):
         assert float(cos) > 0.999, (name, float(cos))
 
 
+def test_fp16_autocast_with_loss_scaling_tracks_the_fallback_model(gpu):
+    # The fp16 path of the train loop (train_loop.py:154-159: grad_scaler.scale(loss).backward()):
+    # fp16 gate/up, query/key and logits, and a loss gradient equal to the scale, which the
+    # fused cross-entropy applies on the device; gradients compared after unscaling.
+    reference, fused = _models(gpu)
+    ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(5)).to(gpu)
+    scale = 4096.0
+
+    def scaled_step(model, use_fused):
+        loss_fn = CrossEntropyWithFallback(use_triton=use_fused)
+        with torch.autocast("cuda", dtype=torch.float16):
+            logits = model(ids)
+            loss = loss_fn(logits, ids, shift=True)
+        (loss * scale).backward()
+        return loss.detach().float(), {n: p.grad.detach() / scale for n, p in model.named_parameters()}
+
+    with _no_fallback_warning():
+        loss_f, grads_f = scaled_step(fused, True)
+    loss_r, grads_r = scaled_step(reference, False)
+    assert abs(loss_f.item() - loss_r.item()) <= 5e-3 * abs(loss_r.item())
+    for name, g in grads_r.items():
+        assert bool(torch.isfinite(grads_f[name]).all()), name
+        cos = F.cosine_similarity(grads_f[name].flatten().double(), g.flatten().double(), dim=0)
+        assert float(cos) > 0.999, (name, float(cos))
+
+
 @contextlib.contextmanager
 def _no_fallback_warning():
     """Fails if any fused module falls back to PyTorch (its warning says 'PyTorch fallback')."""
