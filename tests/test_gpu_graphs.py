@@ -12,6 +12,11 @@ graph's private pool).
 
 from __future__ import annotations
 
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -231,3 +236,40 @@ def test_clip_table_must_be_built_before_capture(gpu):
             with torch.cuda.graph(graph, stream=side):
                 triton_zero_clip_grad_norm_([p], 1.0)
     torch.cuda.synchronize()
+
+
+_FIRST_LAUNCH_IN_CAPTURE = textwrap.dedent("""
+    import sys
+    sys.path.insert(0, {root!r})
+    import torch
+    from picotron_amd import ops
+    dev = torch.device("cuda:0")
+    n = 1 << 22
+    g, u, dy = (torch.randn(n, device=dev).bfloat16() for _ in range(3))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            dg, du = ops.swiglu_bwd(dy, g, u)
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        g.copy_(torch.randn(n, device=dev).bfloat16())
+        graph.replay()
+        torch.cuda.synchronize()
+        eg, eu = ops.swiglu_bwd(dy, g, u)
+        torch.cuda.synchronize()
+        assert torch.equal(dg, eg) and torch.equal(du, eu), i
+    print("ok")
+""")
+
+
+def test_first_launch_inside_a_capture(gpu):
+    """A fresh process whose first SwiGLU backward launch is captured: that launch raises the
+    kernel's dynamic LDS limit (its occupancy limit needs more than 64 KB) during the capture,
+    and every replay must still equal the eager call."""
+
+    root = str(Path(__file__).resolve().parents[1])
+    proc = subprocess.run([sys.executable, "-c", _FIRST_LAUNCH_IN_CAPTURE.format(root=root)],
+                          capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0 and proc.stdout.strip().endswith("ok"), proc.stdout + proc.stderr
