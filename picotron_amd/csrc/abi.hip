@@ -80,8 +80,10 @@ size_t occupancy_lds(int per_cu, size_t static_lds) {
   if (per_cu <= 0) return 0;
   // Each workgroup takes a 1/per_cu share of the CU's LDS, less a margin that keeps the
   // share above 1/(per_cu + 1) of it (true for per_cu <= 12), so exactly per_cu fit.
-  const size_t share = lds_per_cu() / static_cast<size_t>(per_cu) - 1024;
-  return share > static_lds ? share - static_lds : 0;
+  // Larger per_cu values leave little or no share: the limit then fades to none.
+  const int64_t share = static_cast<int64_t>(lds_per_cu() / static_cast<size_t>(per_cu)) - 1024 -
+                        static_cast<int64_t>(static_lds);
+  return share > 0 ? static_cast<size_t>(share) : 0;
 }
 
 int allow_dynamic_lds(const void* kernel, size_t bytes) {
