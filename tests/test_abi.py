@@ -14,6 +14,11 @@ from picotron_amd import _lib
 HEADER = ROOT / "include" / "picotron_hip.h"
 
 
+# An 8-byte-aligned host record, so that validation reaches the step-table check (nothing is
+# launched: the entry point rejects the missing step table first).
+_HOST_TABLE = (ctypes.c_int64 * 6)()
+
+
 def _declared_functions() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     return set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text))
@@ -63,6 +68,8 @@ def test_workspace_queries():
         ("pt_swiglu_fwd", (None, None, None, -1, 2, None), _lib.PT_EINVAL),
         ("pt_rope", (None, None, None, None, None, None, 7, None, None, 1, 0, 0, 2, None), _lib.PT_EINVAL),
         ("pt_adamw_step", (None, 1, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
+        ("pt_adamw_step_device_step", (None, 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
+        ("pt_adamw_step_device_step", (ctypes.addressof(_HOST_TABLE), 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
         ("pt_copy", (None, None, 16, None), _lib.PT_EINVAL),
         ("pt_cross_entropy", (None, 4, 1, 8, 0, 8, None, 1, 0, -100, None, 0, None, 0, 7, None), _lib.PT_EINVAL),
         ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EINVAL),
@@ -84,6 +91,26 @@ def test_empty_inputs_are_no_ops():
     assert lib.pt_swiglu_fwd(None, None, None, 0, 2, None) == _lib.PT_OK
     assert lib.pt_swiglu_bwd(None, None, None, None, None, 5, 2, None) == _lib.PT_OK
     assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
+    assert lib.pt_adamw_step_device_step(None, 0, 0, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None) == _lib.PT_OK
     assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, 2, None) == _lib.PT_OK
     assert lib.pt_last_error() == b""
 
+
+
+def test_adamw_tables_skip_empty_tensors_in_one_order():
+    import torch
+
+    from picotron_amd import ops
+
+    per = ops.adamw_block_elems()
+    params = [torch.zeros(n) for n in (5, 0, per + 1, 0, 3 * per)]
+    steps = [torch.zeros(()) for _ in params]
+    table, blocks = ops.adamw_table(params, params, params, params)
+    step_table = ops.adamw_step_table(params, steps)
+    kept = [i for i, p in enumerate(params) if p.numel() > 0]
+    assert table.shape == (len(kept), 6) and step_table.shape == (len(kept),)
+    assert table[:, 0].tolist() == [params[i].data_ptr() for i in kept]
+    assert table[:, 4].tolist() == [params[i].numel() for i in kept]
+    assert table[:, 5].tolist() == [0, 1, 3]  # running sums of ceil(numel / block elements)
+    assert blocks == 6
+    assert step_table.tolist() == [steps[i].data_ptr() for i in kept]
