@@ -99,7 +99,7 @@ def test_shapes(gpu, dtype, rows, vocab):
     "dtype,vocab",
     [(torch.bfloat16, 24), (torch.bfloat16, 50264), (torch.float16, 50264), (torch.bfloat16, 128256),
      (torch.float16, 128256), (torch.float32, 65528), (torch.float32, 12), (torch.bfloat16, 151936),
-     (torch.float32, 65540)],
+     (torch.float16, 151936), (torch.bfloat16, 262144), (torch.float32, 65540)],
 )
 def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
     # 16-byte aligned rows (held in registers, or streamed in batches when longer) whose last
@@ -116,7 +116,11 @@ def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
     _check(logits, targets, dtype)
 
 
-@pytest.mark.parametrize("dtype,vocab", [(torch.bfloat16, 50257), (torch.float16, 50257), (torch.float32, 1001)])
+@pytest.mark.parametrize(
+    "dtype,vocab",
+    [(torch.bfloat16, 50257), (torch.float16, 50257), (torch.float32, 1001), (torch.bfloat16, 151939),
+     (torch.float16, 200003)],
+)
 def test_targets_at_the_splits_of_unaligned_rows(gpu, dtype, vocab):
     # Rows whose byte stride is not a multiple of 16 start at varying alignments; each is
     # split into a head before its first 16-byte boundary, a body of 16-byte vectors and a
