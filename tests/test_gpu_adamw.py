@@ -67,6 +67,47 @@ def test_matches_torch_adamw_multi_tensor(gpu):
     assert sd["state"][0]["step"].device.type == "cpu" and float(sd["state"][0]["step"]) == 4.0
 
 
+def test_checkpoint_round_trip_continues_identically(gpu):
+    # picotron saves and restores optimizer.state_dict() (src/picotron/serialize/checkpoint.py:
+    # 50,91): a torch-written state resumes under the fused step, and a fused-written state
+    # resumes under torch's step, each continuing as the other would
+    import copy
+
+    sizes = [(513, 7), (1000,), (1,)]
+
+    def grads(step):
+        return [randn(sz, torch.float32, gpu, 40 * step + i, 1e-3) for i, sz in enumerate(sizes)]
+
+    torch_params = [torch.nn.Parameter(randn(sz, torch.float32, gpu, i, 0.02)) for i, sz in enumerate(sizes)]
+    torch_opt = torch.optim.AdamW(torch_params, foreach=False, **HP)
+    for step in range(2):
+        for p, g in zip(torch_params, grads(step)):
+            p.grad = g
+        torch_opt.step()
+    fused_params = [torch.nn.Parameter(p.detach().clone()) for p in torch_params]
+    fused_opt = torch.optim.AdamW(fused_params, **HP)
+    fused_opt.load_state_dict(copy.deepcopy(torch_opt.state_dict()))
+    for step in (2, 3):
+        for a, b, g in zip(fused_params, torch_params, grads(step)):
+            a.grad, b.grad = g, g.clone()
+        triton_adamw_step(fused_opt)
+        torch_opt.step()
+    # and back: the fused optimizer's state into a fresh torch optimizer
+    resumed = [torch.nn.Parameter(p.detach().clone()) for p in fused_params]
+    resumed_opt = torch.optim.AdamW(resumed, foreach=False, **HP)
+    resumed_opt.load_state_dict(copy.deepcopy(fused_opt.state_dict()))
+    for a, b, g in zip(resumed, torch_params, grads(4)):
+        a.grad, b.grad = g, g.clone()
+    resumed_opt.step()
+    torch_opt.step()
+    for a, b in zip(resumed, torch_params):
+        close_fp32(a.detach(), b.detach())
+        sa, sb = resumed_opt.state[a], torch_opt.state[b]
+        assert float(sa["step"]) == float(sb["step"]) == 5.0
+        close_fp32(sa["exp_avg"], sb["exp_avg"])
+        close_fp32(sa["exp_avg_sq"], sb["exp_avg_sq"])
+
+
 def test_unaligned_views_and_missing_grads(gpu):
     flat = randn((10_001,), torch.float32, gpu, 9, 0.02)
     params = [torch.nn.Parameter(flat[1:5000].clone()), torch.nn.Parameter(flat[:7].clone())]
