@@ -212,8 +212,9 @@ constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000
 //      vector store of that address, the target element (softmax_t - 1) / n_valid.
 // Keeping e rounds the softmax twice in 16-bit storage (once as e, once as the gradient),
 // a relative error of at most 2 units of the storage type's last place.
-// The launch guarantees VPT is the smallest of 1, 2, 4, 8, 16 that covers the row, so the
-// vectors of chunks k < VPT / 2 are always inside it.
+// The launch picks the smallest VPT of 1, 2, 3, 4, 6, 8, 10, 12, 14, 16 that covers the row;
+// each is at most twice the one before, so the vectors of chunks k < VPT / 2 are always
+// inside it.
 template <typename T, int VPT>
 __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
@@ -733,8 +734,13 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
   }
     PT_CE_CASE(1)
     PT_CE_CASE(2)
+    PT_CE_CASE(3)
     PT_CE_CASE(4)
+    PT_CE_CASE(6)
     PT_CE_CASE(8)
+    PT_CE_CASE(10)
+    PT_CE_CASE(12)
+    PT_CE_CASE(14)
     PT_CE_CASE(16)
 #undef PT_CE_CASE
   }
