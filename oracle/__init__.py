@@ -1,9 +1,9 @@
 """Oracle: a CPU-checkable restatement of the reference algorithms (TEST INFRASTRUCTURE).
 
-This package is the checker, not the product.  Only ``tests/``, ``__graft_entry__.smoke()``
-and the ``cpu_baseline`` leg of ``bench.py`` may import it; nothing in ``picotron_amd``
-does.  Each function restates AndyMLAndAI/picotron's PyTorch path for one op and cites the
-reference file:line it follows:
+This package is what the tests compare against, not the product.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it;
+nothing in ``picotron_amd`` does.  Each function restates AndyMLAndAI/picotron's PyTorch
+path for one op and cites the reference file:line it follows:
 
   rmsnorm        src/picotron/nn/triton_kernels/rmsnorm.py:49-60, 96-134
   swiglu         src/picotron/nn/triton_kernels/swiglu.py:59-81; src/picotron/nn/feedforward.py:26-43
