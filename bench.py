@@ -962,7 +962,7 @@ def main() -> int:
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the kernels run on a single MI355X and this build has "
+        print("bench.py measures one GPU: the kernels run on a single MI355X and the library has "
               "no multi-GPU path (run with --gpus 1).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

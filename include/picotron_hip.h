@@ -38,7 +38,7 @@ extern "C" {
 /* return codes */
 #define PT_OK 0
 #define PT_EINVAL 1        /* bad argument: null pointer, shape, stride, alignment */
-#define PT_EUNSUPPORTED 2  /* valid request this build does not handle (dtype, size) */
+#define PT_EUNSUPPORTED 2  /* valid request the library does not handle (dtype, size) */
 #define PT_ELAUNCH 3       /* hipGetLastError() reported a launch failure */
 #define PT_EDEVICE 4       /* no usable gfx950 device / HIP runtime error */
 
