@@ -92,6 +92,31 @@ def test_strided_unaligned_and_gqa(gpu):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
+def test_fused_qkv_projection_views(gpu, layout):
+    # q and k as views of one fused QKV projection output (B, S, (Hq + 2 Hkv) * D): their
+    # sequence stride spans every head of q, k and v, and k starts Hq * D elements in
+    from picotron_amd.nn.triton_kernels import triton_apply_rotary_embedding_pair
+
+    b, s, hq, hkv, d = 2, 40, 8, 2, 128
+    width = (hq + 2 * hkv) * d
+    qkv = randn((b, s, width), torch.bfloat16, gpu, 21).requires_grad_(True)
+    q = qkv[..., : hq * d].view(b, s, hq, d).transpose(1, 2)
+    k = qkv[..., hq * d : (hq + hkv) * d].view(b, s, hkv, d).transpose(1, 2)
+    cos, sin = o_rope.tables(s, d, 500_000.0, device=gpu)
+    rq, rk = triton_apply_rotary_embedding_pair(q, k, cos, sin, layout=layout)
+    torch.testing.assert_close(rq.double(), o_rope.rotate(q.detach(), cos, sin, layout), **BF16)
+    torch.testing.assert_close(rk.double(), o_rope.rotate(k.detach(), cos, sin, layout), **BF16)
+    gq = randn(rq.shape, torch.bfloat16, gpu, 22)
+    gk = randn(rk.shape, torch.bfloat16, gpu, 23)
+    torch.autograd.backward((rq, rk), (gq, gk))
+    want = torch.zeros((b, s, width), dtype=torch.float64, device=gpu)
+    want[..., : hq * d] = o_rope.rotate(gq, cos, sin, layout, inverse=True).transpose(1, 2).reshape(b, s, hq * d)
+    want[..., hq * d : (hq + hkv) * d] = (
+        o_rope.rotate(gk, cos, sin, layout, inverse=True).transpose(1, 2).reshape(b, s, hkv * d))
+    torch.testing.assert_close(qkv.grad.double(), want, **BF16)  # v's columns get no gradient
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_autograd_surface_and_module(gpu, layout):
     import warnings
 
