@@ -67,6 +67,50 @@ def test_matches_torch_adamw_multi_tensor(gpu):
     assert sd["state"][0]["step"].device.type == "cpu" and float(sd["state"][0]["step"]) == 4.0
 
 
+def test_param_groups_late_group_and_fused_clip(gpu):
+    # Several groups with their own hyperparameters, a group added after two steps (its
+    # parameters count their own steps: one launch per distinct step value), a parameter
+    # without a gradient, and the clip's norm taken over every group, against torch
+    def make(seed_base):
+        decay = [torch.nn.Parameter(randn((300, 17), torch.float32, gpu, seed_base + 1, 0.02)),
+                 torch.nn.Parameter(randn((4096,), torch.float32, gpu, seed_base + 2, 0.02))]
+        no_decay = [torch.nn.Parameter(randn((4096,), torch.float32, gpu, seed_base + 3, 0.02)),
+                    torch.nn.Parameter(randn((5,), torch.float32, gpu, seed_base + 4, 0.02))]
+        late = [torch.nn.Parameter(randn((777,), torch.float32, gpu, seed_base + 5, 0.02))]
+        return decay, no_decay, late
+
+    fused, ref = make(0), make(0)
+    groups = lambda ps: [dict(params=ps[0], lr=1e-3, weight_decay=0.1),
+                         dict(params=ps[1], lr=5e-4, weight_decay=0.0, betas=(0.8, 0.9), eps=1e-6)]
+    opt_f = torch.optim.AdamW(groups(fused), betas=(0.9, 0.95), eps=1e-8)
+    opt_r = torch.optim.AdamW(groups(ref), betas=(0.9, 0.95), eps=1e-8, foreach=False)
+    stepper = AdamWStepWithFallback(use_triton=True)
+    for step in range(4):
+        if step == 2:
+            opt_f.add_param_group(dict(params=fused[2], lr=2e-3, weight_decay=0.05))
+            opt_r.add_param_group(dict(params=ref[2], lr=2e-3, weight_decay=0.05))
+        for gi, (gf, gr) in enumerate(zip(fused, ref)):
+            for pi, (a, b) in enumerate(zip(gf, gr)):
+                if gi == 1 and pi == 1 and step == 1:
+                    a.grad = b.grad = None  # skipped this step
+                    continue
+                g = randn(a.shape, torch.float32, gpu, 1000 * step + 10 * gi + pi, 0.05)
+                a.grad, b.grad = g, g.clone()
+        stepper.step(opt_f, max_grad_norm=1.0)
+        params_r = [p for ps in (ref if step >= 2 else ref[:2]) for p in ps]
+        torch.nn.utils.clip_grad_norm_(params_r, 1.0)
+        opt_r.step()
+    assert not stepper._fallback_warned
+    for gf, gr in zip(fused, ref):
+        for a, b in zip(gf, gr):
+            close_fp32(a.detach(), b.detach())
+            sa, sb = opt_f.state[a], opt_r.state[b]
+            assert float(sa["step"]) == float(sb["step"])
+            close_fp32(sa["exp_avg"], sb["exp_avg"])
+            close_fp32(sa["exp_avg_sq"], sb["exp_avg_sq"])
+    assert float(opt_f.state[fused[2][0]]["step"]) == 2.0 and float(opt_f.state[fused[1][1]]["step"]) == 3.0
+
+
 def test_checkpoint_round_trip_continues_identically(gpu):
     # picotron saves and restores optimizer.state_dict() (src/picotron/serialize/checkpoint.py:
     # 50,91): a torch-written state resumes under the fused step, and a fused-written state
