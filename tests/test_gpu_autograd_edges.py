@@ -1,0 +1,84 @@
+"""Autograd edge cases of the fused ops: the upstream gradient of ``out.sum()`` is a
+stride-0 expanded tensor, and ``out[..., ::2].sum()`` a strided one; the fused backward must
+give the fallback's gradients (fp32, tolerance of the fp32 parity tests)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import close_fp32, randn
+from oracle import rope as o_rope
+from picotron_amd.nn.triton_kernels import (
+    rms_norm_with_pytorch_forward,
+    triton_apply_rotary_embedding,
+    triton_residual_rms_norm,
+    triton_rms_norm,
+    swiglu_with_pytorch_forward,
+    triton_swiglu,
+)
+from picotron_amd.nn.rope import apply_rotary_embedding
+
+pytestmark = pytest.mark.gpu
+
+REDUCTIONS = {
+    "sum": lambda y: y.sum(),  # expanded (stride 0) upstream gradient
+    "strided": lambda y: (y[..., ::2] * 1.5).sum(),  # gradient with zeros at odd columns
+}
+
+
+def _grads(fn, *inputs):
+    leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+    out = fn(*leaves)
+    return out, leaves
+
+
+@pytest.mark.parametrize("reduce", list(REDUCTIONS))
+def test_rmsnorm(gpu, reduce):
+    x = randn((6, 33, 200), torch.float32, gpu, 1)
+    w = randn((200,), torch.float32, gpu, 2, 0.1, 1.0)
+    y_f, (xf, wf) = _grads(lambda a, b: triton_rms_norm(a, b, 1e-6), x, w)
+    y_r, (xr, wr) = _grads(lambda a, b: rms_norm_with_pytorch_forward(a, b, 1e-6), x, w)
+    REDUCTIONS[reduce](y_f).backward()
+    REDUCTIONS[reduce](y_r).backward()
+    close_fp32(xf.grad, xr.grad, scale=float(xr.grad.abs().max()) * 10)
+    close_fp32(wf.grad, wr.grad)
+
+
+@pytest.mark.parametrize("reduce", list(REDUCTIONS))
+def test_residual_rmsnorm(gpu, reduce):
+    x, r = randn((5, 64), torch.float32, gpu, 3), randn((5, 64), torch.float32, gpu, 4)
+    w = randn((64,), torch.float32, gpu, 5, 0.1, 1.0)
+    outs, (xf, rf, wf) = _grads(lambda a, b, c: triton_residual_rms_norm(a, b, c, 1e-6), x, r, w)
+
+    def ref(a, b, c):
+        h = a + b
+        return h, rms_norm_with_pytorch_forward(h, c, 1e-6)
+
+    refs, (xr, rr, wr) = _grads(ref, x, r, w)
+    (REDUCTIONS[reduce](outs[0]) + REDUCTIONS[reduce](outs[1])).backward()
+    (REDUCTIONS[reduce](refs[0]) + REDUCTIONS[reduce](refs[1])).backward()
+    for a, b in ((xf, xr), (rf, rr), (wf, wr)):
+        close_fp32(a.grad, b.grad, scale=float(b.grad.abs().max()) * 10)
+
+
+@pytest.mark.parametrize("reduce", list(REDUCTIONS))
+def test_swiglu(gpu, reduce):
+    g, u = randn((7, 130), torch.float32, gpu, 6), randn((7, 130), torch.float32, gpu, 7)
+    y_f, (gf, uf) = _grads(triton_swiglu, g, u)
+    y_r, (gr, ur) = _grads(swiglu_with_pytorch_forward, g, u)
+    REDUCTIONS[reduce](y_f).backward()
+    REDUCTIONS[reduce](y_r).backward()
+    close_fp32(gf.grad, gr.grad)
+    close_fp32(uf.grad, ur.grad)
+
+
+@pytest.mark.parametrize("reduce", list(REDUCTIONS))
+def test_rope(gpu, reduce):
+    x = randn((2, 3, 19, 32), torch.float32, gpu, 8)
+    cos, sin = o_rope.tables(19, 32, 10_000.0, device=gpu)
+    y_f, (xf,) = _grads(lambda a: triton_apply_rotary_embedding(a, cos, sin), x)
+    y_r, (xr,) = _grads(lambda a: apply_rotary_embedding(a, cos, sin), x)
+    REDUCTIONS[reduce](y_f).backward()
+    REDUCTIONS[reduce](y_r).backward()
+    close_fp32(xf.grad, xr.grad)
