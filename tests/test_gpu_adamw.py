@@ -111,6 +111,41 @@ def test_param_groups_late_group_and_fused_clip(gpu):
     assert float(opt_f.state[fused[2][0]]["step"]) == 2.0 and float(opt_f.state[fused[1][1]]["step"]) == 3.0
 
 
+@pytest.mark.parametrize(
+    "options",
+    [dict(amsgrad=True), dict(maximize=True), dict(lr=torch.tensor(1e-3)), dict(fused=True)],
+    ids=["amsgrad", "maximize", "tensor_lr", "torch_fused"],
+)
+def test_unsupported_options_fall_back_to_torch(gpu, options):
+    # Options the fused step does not implement: the step raises TritonAdamWUnavailable
+    # before touching any state, AdamWStepWithFallback warns once and runs torch's own
+    # step, and the result equals torch's
+    import warnings
+
+    from picotron_amd.nn.triton_kernels import TritonAdamWUnavailable
+
+    hp = dict(HP, **options)
+    if "lr" in options:
+        hp["lr"] = torch.tensor(1e-3)
+    fused = [torch.nn.Parameter(randn((1000,), torch.float32, gpu, 1, 0.02))]
+    ref = [torch.nn.Parameter(fused[0].detach().clone())]
+    opt_f, opt_r = torch.optim.AdamW(fused, **hp), torch.optim.AdamW(ref, **hp)
+    g = randn((1000,), torch.float32, gpu, 2, 1e-3)
+    fused[0].grad, ref[0].grad = g, g.clone()
+    with pytest.raises(TritonAdamWUnavailable, match="not implemented"):
+        triton_adamw_step(opt_f)
+    assert len(opt_f.state) == 0  # nothing touched
+    stepper = AdamWStepWithFallback(use_triton=True)
+    with warnings.catch_warnings(record=True) as records:
+        warnings.simplefilter("always")
+        stepper.step(opt_f)
+        stepper.step(opt_f)
+    assert sum("Triton AdamW unavailable" in str(w.message) for w in records) == 1
+    opt_r.step()
+    opt_r.step()
+    assert torch.equal(fused[0].detach(), ref[0].detach())
+
+
 def test_checkpoint_round_trip_continues_identically(gpu):
     # picotron saves and restores optimizer.state_dict() (src/picotron/serialize/checkpoint.py:
     # 50,91): a torch-written state resumes under the fused step, and a fused-written state
