@@ -110,25 +110,16 @@ int64_t env_int(const char* name, int64_t fallback) {
   return (end != v && x >= 0) ? static_cast<int64_t>(x) : fallback;
 }
 
-// Grid-stride 16-byte copy; UNROLL independent vectors in flight per thread.
-template <int UNROLL>
+// 16-byte nontemporal copy.  One-shot grid: thread t of block b moves vector b*256 + t, so
+// every vector has its own thread and the grid drains once (measured on MI355X over 1 GiB:
+// 6.46 TB/s, against 5.99 TB/s for a grid-stride loop over 32 workgroups per CU with four
+// vectors in flight per thread).  `base` offsets the grid for copies of more vectors than
+// one launch's work-item count can address.
 __global__ __launch_bounds__(256) void copy16_kernel(const u32x4* __restrict__ src,
-                                                     u32x4* __restrict__ dst, int64_t nvec) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x * UNROLL;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * UNROLL + threadIdx.x;
-       base < nvec; base += stride) {
-    u32x4 v[UNROLL];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
-      if (i < nvec) v[u] = __builtin_nontemporal_load(src + i);
-    }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      int64_t i = base + static_cast<int64_t>(u) * blockDim.x;
-      if (i < nvec) __builtin_nontemporal_store(v[u], dst + i);
-    }
-  }
+                                                     u32x4* __restrict__ dst, int64_t base,
+                                                     int64_t nvec) {
+  const int64_t i = base + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < nvec) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* __restrict__ p, int64_t n,
@@ -182,14 +173,17 @@ int pt_copy(const void* src, void* dst, int64_t bytes, void* stream) {
   if (!pt::aligned16(src) || !pt::aligned16(dst))
     return pt::fail(PT_EINVAL, "pt_copy: pointers must be 16-byte aligned");
   if (bytes == 0) return pt::ok();
-  constexpr int kUnroll = 4;
   const int64_t nvec = bytes / 16;
-  int64_t blocks = (nvec + 256 * kUnroll - 1) / (256 * kUnroll);
-  const int64_t cap = static_cast<int64_t>(pt::num_cus()) * 32;
-  if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL(pt::copy16_kernel<kUnroll>, dim3(static_cast<unsigned>(blocks)), dim3(256),
-                     0, pt::as_stream(stream), reinterpret_cast<const pt::u32x4*>(src),
-                     reinterpret_cast<pt::u32x4*>(dst), nvec);
+  // A launch addresses fewer than 2^32 work-items: 2^23 workgroups (2^31 vectors, 32 GiB)
+  // per launch.
+  constexpr int64_t kChunk = int64_t{1} << 31;
+  for (int64_t base = 0; base < nvec; base += kChunk) {
+    const int64_t n = nvec - base < kChunk ? nvec - base : kChunk;
+    hipLaunchKernelGGL(pt::copy16_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                       0, pt::as_stream(stream), reinterpret_cast<const pt::u32x4*>(src),
+                       reinterpret_cast<pt::u32x4*>(dst), base, nvec);
+    if (int rc = pt::check_launch("pt_copy")) return rc;
+  }
   return pt::check_launch("pt_copy");
 }
 
