@@ -79,6 +79,20 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
                    void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
                    int64_t cols, int x_dtype, int w_dtype, void* stream);
 
+/* pt_rmsnorm_bwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The weight-gradient partials go to a
+ * static device array of the library (16 MiB, one per device, held until the process
+ * ends); the call allocates and frees nothing.  Same arguments and results as
+ * pt_rmsnorm_bwd (bitwise: same kernels and grid).  Returns PT_EUNSUPPORTED when the
+ * partials, pt_rmsnorm_bwd_workspace_bytes(rows, cols, x_dtype), exceed 16 MiB (e.g. more
+ * than 8192 columns at 16384 rows).  Calls that overlap on one device share the array and
+ * race: issue them on one stream, or serialise them. */
+int pt_rmsnorm_bwd_noalloc(const void* dy, int64_t dy_row_stride, const void* x,
+                           int64_t x_row_stride, const void* weight, const float* rstd, void* dx,
+                           int64_t dx_row_stride, void* dweight, int64_t rows, int64_t cols,
+                           int x_dtype, int w_dtype, void* stream);
+
 /* Residual add fused with the norm that follows it in the decoder block
  * (src/picotron/models/picotron_decoder.py:116-119: hidden = hidden + attention(...), then
  * mlp_norm(hidden)):  h = x + residual, computed in fp32 and rounded to x's type, is written,

@@ -46,6 +46,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
          c_void_p, c_size_t, c_int64, c_int64, c_int, c_int, c_void_p],
     ),
+    "pt_rmsnorm_bwd_noalloc": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+         c_int64, c_int64, c_int, c_int, c_void_p],
+    ),
     "pt_residual_rmsnorm_fwd": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64,

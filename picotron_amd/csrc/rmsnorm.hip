@@ -1,5 +1,6 @@
 // C ABI of the RMSNorm kernels: argument validation, shape/alignment selection, and
 // the deterministic weight-gradient finish pass.  Kernels live in rmsnorm_impl.hpp.
+#include <mutex>
 #include <string>
 
 #include "rmsnorm_impl.hpp"
@@ -129,7 +130,7 @@ int fwd_impl(const char* fn, const void* x, int64_t xs, const void* res, int64_t
 int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int64_t dh_in_s,
              const void* x, int64_t xs, const void* weight, const float* rstd, void* dx,
              int64_t dxs, void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
-             int64_t cols, int x_dtype, int w_dtype, void* stream) {
+             int64_t cols, int x_dtype, int w_dtype, void* stream, bool static_scratch = false) {
   const std::string name(fn);
   Shape s;
   if (int rc = validate(fn, rows, cols, x_dtype, w_dtype, true, &s)) return rc;
@@ -154,6 +155,11 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
   float* partial = nullptr;
   if (dweight) {
     const size_t need = static_cast<size_t>(a.blocks) * static_cast<size_t>(cols) * sizeof(float);
+    if (static_scratch && need > workspace_bytes)
+      return fail(PT_EUNSUPPORTED,
+                  name + ": the weight-gradient partials need " + std::to_string(need) +
+                      " bytes, more than the library's static scratch of " +
+                      std::to_string(workspace_bytes) + " bytes; use pt_rmsnorm_bwd");
     if (!workspace || workspace_bytes < need)
       return fail(PT_EINVAL, name + ": workspace smaller than pt_rmsnorm_bwd_workspace_bytes()");
     if (!aligned16(workspace)) return fail(PT_EINVAL, name + ": workspace not aligned");
@@ -201,6 +207,47 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
 }  // namespace rmsnorm
 }  // namespace pt
 
+namespace pt {
+namespace rmsnorm {
+
+// Scratch of pt_rmsnorm_bwd_noalloc: the fp32 weight-gradient partial rows, [blocks, cols]
+// (512 x 4096 at 16384 x 4096, 8 MiB).  A file-scope device array, so that entry point
+// allocates nothing; every device the library runs on holds one copy until the process
+// ends.  Each call overwrites every partial it reads (each block writes its whole row), so
+// nothing needs clearing between calls; calls that overlap on one device race on it.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_err[kScratchDevices];
+
+// Device address of the current device's copy of `scratch`, looked up once per device with
+// that device current.  In host code the array's name is only a host-side stand-in for the
+// symbol: kernels and copies must be given this address instead.
+int scratch_address(const char* fn, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return fail(PT_EDEVICE, std::string(fn) + ": no current HIP device");
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
+    return fail(PT_EDEVICE, std::string(fn) + ": hipGetSymbolAddress(scratch) failed: " +
+                                hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return PT_OK;
+}
+
+}  // namespace
+}  // namespace rmsnorm
+}  // namespace pt
+
 using namespace pt;
 using namespace pt::rmsnorm;
 
@@ -233,6 +280,20 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
   return bwd_impl("pt_rmsnorm_bwd", dy, dy_row_stride, nullptr, 0, x, x_row_stride, weight, rstd,
                   dx, dx_row_stride, dweight, workspace, workspace_bytes, rows, cols, x_dtype,
                   w_dtype, stream);
+}
+
+int pt_rmsnorm_bwd_noalloc(const void* dy, int64_t dy_row_stride, const void* x,
+                           int64_t x_row_stride, const void* weight, const float* rstd, void* dx,
+                           int64_t dx_row_stride, void* dweight, int64_t rows, int64_t cols,
+                           int x_dtype, int w_dtype, void* stream) {
+  static const char* const fn = "pt_rmsnorm_bwd_noalloc";
+  void* ws = nullptr;
+  if (dweight != nullptr && rows > 0) {
+    if (int rc = scratch_address(fn, &ws)) return rc;
+  }
+  return bwd_impl(fn, dy, dy_row_stride, nullptr, 0, x, x_row_stride, weight, rstd, dx,
+                  dx_row_stride, dweight, ws, ws ? kScratchBytes : 0, rows, cols, x_dtype, w_dtype,
+                  stream, true);
 }
 
 int pt_residual_rmsnorm_fwd(const void* x, int64_t x_row_stride, const void* residual,
