@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 1
+#define PT_ABI_VERSION 2
 
 /* element type codes (storage types; arithmetic is always fp32) */
 #define PT_FLOAT32 0
@@ -158,7 +158,12 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
  * outer=B, inner=S-1, outer_stride=S*V, inner_stride=V.
  * loss_out (fp32 scalar, device) = sum(lse - logit[target]) / n_valid.
  * If write_grad != 0 the logits are overwritten IN PLACE with
- *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows).
+ *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows)
+ * for fp32 and bf16.  fp16 logits receive (softmax - onehot(target)) * 2^15 * q / n_valid
+ * instead, q the largest power of two not above n_valid: the loss scale of fp16 training
+ * arrives only with the backward, and softmax / n_valid is mostly below fp16's smallest
+ * subnormal at language-model sizes.  The fp16 gradient is complete once
+ * pt_cross_entropy_scale_grad has run (always needed for fp16).
  * A non-ignored target outside [0, vocab) makes that row's loss NaN and sets
  * *(int32*)status bit 0; status is part of the workspace (see below).
  * Replaces CrossEntropyWithFallback / triton_cross_entropy
@@ -177,12 +182,17 @@ int32_t* pt_cross_entropy_status(void* workspace);
 /* Multiply a gradient written by pt_cross_entropy (same row and target description) by
  * the fp32 scalar at *grad_output (device memory), skipping all work when it equals 1.0
  * exactly; rows whose target is ignore_index stay zero.  This is the backward of the fused
- * loss: the logits already hold d(mean loss)/d(logits). */
+ * loss: the logits already hold d(mean loss)/d(logits).  For fp16 the rows hold
+ * (softmax - onehot) * 2^15 * q / n_valid and are multiplied by *grad_output * 2^-15 / q in
+ * fp32, then rounded to fp16 (always, also for a grad_output of 1; an exact rescaling when
+ * grad_output is a power of two); n_valid is read from `workspace`, the forward call's
+ * workspace, which must then be non-NULL (fp32 and bf16 ignore it). */
 int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
                                 int64_t outer_stride, int64_t inner_stride, int64_t vocab,
                                 const int64_t* targets, int64_t t_outer_stride,
                                 int64_t t_inner_stride, int64_t ignore_index,
-                                const float* grad_output, int dtype, void* stream);
+                                const float* grad_output, const void* workspace, int dtype,
+                                void* stream);
 
 /* Next-token cross-entropy on the whole (batch, seq, vocab) logits of a language model:
  * row (b, t) with t < seq-1 has target input_ids[b*ids_batch_stride + (t+1)*ids_seq_stride];
@@ -201,12 +211,13 @@ int pt_cross_entropy_shifted(void* logits, int64_t batch, int64_t seq, int64_t b
                              void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
 /* pt_cross_entropy_scale_grad for a gradient written by pt_cross_entropy_shifted (same
- * description); the last position and ignored rows stay zero. */
+ * description, same fp16 rule and workspace); the last position and ignored rows stay zero. */
 int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq,
                                         int64_t batch_stride, int64_t seq_stride, int64_t vocab,
                                         const int64_t* input_ids, int64_t ids_batch_stride,
                                         int64_t ids_seq_stride, int64_t ignore_index,
-                                        const float* grad_output, int dtype, void* stream);
+                                        const float* grad_output, const void* workspace,
+                                        int dtype, void* stream);
 
 /* ---------------------------------------------------------------- AdamW
  * One decoupled-weight-decay Adam step over many fp32 tensors in one launch, with

@@ -193,6 +193,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(void* base, int byt
 template <typename T>
 constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
 
+// Scale of the gradient the row kernels write.  fp32 and bf16 rows receive d(mean loss) /
+// d(logits) = (softmax - onehot) / n_valid itself.  fp16 rows receive
+// (softmax - onehot) * 2^15 * q / n_valid, q the largest power of two not above n_valid (a
+// factor in (2^14, 2^15]): a GradScaler's loss scale only arrives with the backward, and
+// softmax / n_valid (about 1e-10 for vocab 128256 over 8192 rows) lies below fp16's smallest
+// subnormal, so stored unscaled nearly every gradient would be 0 before that scale could
+// lift it.  The factor keeps probabilities down to 2^-28 normal (|softmax - onehot| <= 1
+// keeps the values at most 32768 < 65504).  The backward always runs for fp16 and multiplies
+// by grad_output * 2^-15 / q: for a power-of-two grad_output (a GradScaler's scale, or 1) an
+// exact rescaling, so the gradient is rounded no more often than on the other types.
+constexpr float kF16GradScale = 32768.0f;
+
+// The largest power of two not above n (n >= 1): n with its mantissa bits cleared.
+__device__ __forceinline__ float pow2_floor(float n) {
+  return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, n) & 0xff800000u);
+}
+
+template <typename T>
+__device__ __forceinline__ float grad_factor(const CeWork* ws) {
+  if constexpr (std::is_same<T, _Float16>::value) {
+    return (kF16GradScale * pow2_floor(ws->n_valid)) / ws->n_valid;
+  } else {
+    return inv_n_of(ws);
+  }
+}
+
 // The bit pattern of two / one -inf in the storage type, for masking vectors past the row.
 template <typename T>
 constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000u
@@ -317,11 +343,11 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   if (tid == owner) row_losses(ws)[row] = row_loss(M, S, xt);
   if (!write_grad) return;
 
-  const float scale = inv_n_of(ws) / S;
+  const float scale = grad_factor<T>(ws) / S;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     Vec16<T> out;
-    // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf (it held only
+    // exp(m_k - M) / (S n) per chunk (2^15 / S for fp16); 0 for a chunk whose reference is -inf (it held only
     // -inf logits, whose exps are 0).
     const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
 #pragma unroll
@@ -335,7 +361,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
   if (!bad && tid == owner) {
     Vec16<T> one;
-    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n_of(ws)));
+    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, grad_factor<T>(ws)));
     const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
     if constexpr (sizeof(T) == 4) {
       __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
@@ -487,7 +513,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   if (tid == 0) row_losses(ws)[row] = row_loss(M, S, xt);
   if (!write_grad) return;
 
-  const float inv_n = inv_n_of(ws);
+  const float inv_n = grad_factor<T>(ws);
   const float scale = inv_n / S;
 #pragma unroll
   for (int k = 0; k < KEEP; ++k) {
@@ -594,7 +620,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
   if (threadIdx.x == 0) row_losses(ws)[blockIdx.x] = row_loss(mx, se, xt);
   if (!write_grad) return;
 
-  const float inv_n = 1.0f / ws->n_valid;
+  const float inv_n = grad_factor<T>(ws);
   const float scale = inv_n / se;
   const float gt = target_grad(mx, se, xt, inv_n);
   for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
@@ -623,7 +649,9 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
   if (threadIdx.x == 0) *loss_out = total / ws->n_valid;
 }
 
-// In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1.
+// In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1, except
+// for fp16, whose rows hold (softmax - onehot) * 2^15 * q / n_valid and are multiplied by
+// grad_output * 2^-15 / q (n_valid from the forward's workspace).
 // Ignored rows stay zero whatever the scalar is (torch's nll_loss backward leaves them 0).
 // The work items are (row, chunk of 1024 vectors or elements); a grid of up to 128 blocks
 // per CU walks them (a one-shot grid streams no faster and makes the common
@@ -639,10 +667,16 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
                                                        const int64_t* __restrict__ targets,
                                                        int64_t tos, int64_t tis,
                                                        int64_t ignore_index,
-                                                       const float* __restrict__ scale) {
+                                                       const float* __restrict__ scale,
+                                                       const CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
-  const float sc = *scale;
-  if (sc == 1.0f) return;
+  float sc = *scale;
+  if constexpr (std::is_same<T, _Float16>::value) {
+    // power-of-two divisions: exact
+    sc = (sc * (1.0f / kF16GradScale)) / pow2_floor(ws->n_valid);
+  } else {
+    if (sc == 1.0f) return;
+  }
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     const int64_t row = item / chunks;
     const int64_t c = item - row * chunks;
@@ -820,7 +854,8 @@ int ce_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_
 }
 
 template <typename T, bool ALIGNED>
-void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, hipStream_t st) {
+void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, const CeWork* ws,
+                     hipStream_t st) {
   // (row, chunk of 256 * kScaleVecs body vectors) items; a row's body has at most
   // vocab / VEC vectors whether or not it is aligned.
   constexpr int64_t kChunk = 256 * Elem<T>::VEC * kScaleVecs;
@@ -836,21 +871,21 @@ void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, hi
   if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, st, static_cast<T*>(d.logits), d.inner,
                      d.valid_inner, d.os, d.is, d.vocab, items, chunks, d.targets, d.tos, d.tis,
-                     d.ignore_index, grad_output);
+                     d.ignore_index, grad_output, ws);
 }
 
 template <typename T>
 void scale_launch(bool aligned, const CeRows& d, int64_t rows, const float* grad_output,
-                  hipStream_t st) {
+                  const CeWork* ws, hipStream_t st) {
   if (aligned) {
-    scale_launch_as<T, true>(d, rows, grad_output, st);
+    scale_launch_as<T, true>(d, rows, grad_output, ws, st);
   } else {
-    scale_launch_as<T, false>(d, rows, grad_output, st);
+    scale_launch_as<T, false>(d, rows, grad_output, ws, st);
   }
 }
 
 int ce_scale_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_t vocab,
-                 const float* grad_output, int dtype, void* stream) {
+                 const float* grad_output, const void* workspace, int dtype, void* stream) {
   const std::string name(fn);
   if (!valid_dtype(dtype)) return fail(PT_EINVAL, name + ": unknown dtype");
   if (outer < 0 || inner < 0 || vocab <= 0 || vocab > (int64_t{1} << 30))
@@ -859,17 +894,20 @@ int ce_scale_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, 
   if (rows == 0) return ok();
   if (!d.logits || (d.valid_inner > 0 && !d.targets) || !grad_output)
     return fail(PT_EINVAL, name + ": null pointer");
+  if (dtype == PT_FLOAT16 && (workspace == nullptr || !aligned16(workspace)))
+    return fail(PT_EINVAL, name + ": fp16 gradients need the forward's workspace (16-byte aligned)");
+  const CeWork* ws = static_cast<const CeWork*>(workspace);
   hipStream_t st = as_stream(stream);
   const int esize = dtype_size(dtype);
   const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
                        (outer <= 1 || (d.os * esize) % 16 == 0) &&
                        (inner <= 1 || (d.is * esize) % 16 == 0);
   if (dtype == PT_FLOAT32) {
-    scale_launch<float>(aligned, d, rows, grad_output, st);
+    scale_launch<float>(aligned, d, rows, grad_output, ws, st);
   } else if (dtype == PT_FLOAT16) {
-    scale_launch<_Float16>(aligned, d, rows, grad_output, st);
+    scale_launch<_Float16>(aligned, d, rows, grad_output, ws, st);
   } else {
-    scale_launch<__bf16>(aligned, d, rows, grad_output, st);
+    scale_launch<__bf16>(aligned, d, rows, grad_output, ws, st);
   }
   return check_launch(fn);
 }
@@ -907,13 +945,14 @@ int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
                                 int64_t outer_stride, int64_t inner_stride, int64_t vocab,
                                 const int64_t* targets, int64_t t_outer_stride,
                                 int64_t t_inner_stride, int64_t ignore_index,
-                                const float* grad_output, int dtype, void* stream) {
+                                const float* grad_output, const void* workspace, int dtype,
+                                void* stream) {
   const int64_t inner_nz = inner > 0 ? inner : 1;
   const CeRows d{logits, inner_nz, inner_nz, outer_stride, inner_stride,
                  static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
                  targets, t_outer_stride, t_inner_stride, ignore_index};
-  return ce_scale_run("pt_cross_entropy_scale_grad", d, outer, inner, vocab, grad_output, dtype,
-                      stream);
+  return ce_scale_run("pt_cross_entropy_scale_grad", d, outer, inner, vocab, grad_output,
+                      workspace, dtype, stream);
 }
 
 // Rows (b, t) of (batch, seq, vocab) logits; row t < seq - 1 predicts input_ids[b, t + 1], so
@@ -944,11 +983,12 @@ int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq
                                         int64_t batch_stride, int64_t seq_stride, int64_t vocab,
                                         const int64_t* input_ids, int64_t ids_batch_stride,
                                         int64_t ids_seq_stride, int64_t ignore_index,
-                                        const float* grad_output, int dtype, void* stream) {
+                                        const float* grad_output, const void* workspace,
+                                        int dtype, void* stream) {
   const CeRows d = shifted_rows(logits, seq, batch_stride, seq_stride, vocab, input_ids,
                                 ids_batch_stride, ids_seq_stride, ignore_index);
   return ce_scale_run("pt_cross_entropy_shifted_scale_grad", d, batch, seq, vocab, grad_output,
-                      dtype, stream);
+                      workspace, dtype, stream);
 }
 
 }  // extern "C"

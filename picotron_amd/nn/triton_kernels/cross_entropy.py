@@ -9,10 +9,19 @@ the logits require grad, writes d(loss)/d(logits) into the logits' storage durin
 forward (one HBM read + one write of the logits in total).  The backward only rescales by
 the incoming gradient, on device, and skips even that when it is exactly 1.
 
-In-place contract: after a grad-enabled call the logits tensor holds the gradient, not
-the logits.  Its autograd version counter is bumped, so any other graph node that saved
-those logits fails loudly at backward instead of reading wrong values.  Pass
-``inplace=False`` to keep the logits (the gradient then goes to a copy).
+In-place contract of ``triton_cross_entropy`` (default ``inplace=True``): after a
+grad-enabled call the logits tensor holds the gradient, not the logits.  Its autograd
+version counter is bumped, so any other graph node that saved those logits fails loudly at
+backward instead of reading wrong values; a plain read of the tensor after the loss (metrics,
+logging) would see the gradient.  ``inplace=False`` keeps the logits (the gradient then goes
+to a copy), and is the default of ``CrossEntropyWithFallback``, the drop-in for
+``F.cross_entropy``.  Logits whose rows overlap in memory (e.g. an expanded tensor) are
+refused when the gradient would be written into them.  fp16 logits hold
+(softmax - onehot) * 2^15 * q / n_valid between the forward and the backward (q the largest
+power of two not above n_valid), which multiplies by grad_output * 2^-15 / q: the loss
+scale of fp16 training arrives only with the backward, and softmax / n_valid would mostly
+be below fp16's smallest subnormal.  The gradient buffer is
+consumed by the backward, so a second backward through the same graph raises.
 
 ``shift=True`` takes the language model's whole (B, S, V) logits and the (B, S) input ids
 and computes the train loop's next-token loss (reference
@@ -28,6 +37,7 @@ import warnings
 
 import torch
 from torch import Tensor
+from torch.autograd.function import once_differentiable
 from torch.nn import functional as F
 
 from picotron_amd import ops
@@ -41,6 +51,13 @@ class TritonCrossEntropyUnavailable(RuntimeError):
     """Raised when the fused (HIP) cross-entropy path cannot safely run."""
 
 
+_REPEATED_BACKWARD = (
+    "the fused cross-entropy's gradient buffer was consumed by an earlier backward through "
+    "this graph (retain_graph=True); backpropagate through the loss once, or compute it with "
+    "F.cross_entropy"
+)
+
+
 class _FusedCrossEntropy(torch.autograd.Function):
     @staticmethod
     def forward(ctx, logits: Tensor, targets: Tensor, ignore_index: int, inplace: bool):  # type: ignore[override]
@@ -48,20 +65,24 @@ class _FusedCrossEntropy(torch.autograd.Function):
         buffer = logits.detach()
         if write_grad and not inplace:
             buffer = buffer.clone()
-        loss, _ = ops.cross_entropy(buffer, targets, ignore_index, write_grad=write_grad)
+        loss, ws = ops.cross_entropy(buffer, targets, ignore_index, write_grad=write_grad)
         if write_grad:
             if inplace:
                 torch.autograd.graph.increment_version(logits)
             ctx.grad_buffer = buffer
+            ctx.workspace = ws
             ctx.targets = targets
             ctx.ignore_index = ignore_index
         return loss
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_loss: Tensor):  # type: ignore[override]
-        grad = ctx.grad_buffer
-        ops.cross_entropy_scale_grad(grad, ctx.targets, grad_loss, ctx.ignore_index)
-        del ctx.grad_buffer
+        grad = getattr(ctx, "grad_buffer", None)
+        if grad is None:
+            raise RuntimeError(_REPEATED_BACKWARD)
+        ops.cross_entropy_scale_grad(grad, ctx.targets, grad_loss, ctx.ignore_index, ctx.workspace)
+        ctx.grad_buffer = None
         return grad, None, None, None
 
 
@@ -72,20 +93,25 @@ class _FusedShiftedCrossEntropy(torch.autograd.Function):
         buffer = logits.detach()
         if write_grad and not inplace:
             buffer = buffer.clone()
-        loss, _ = ops.cross_entropy_shifted(buffer, input_ids, ignore_index, write_grad=write_grad)
+        loss, ws = ops.cross_entropy_shifted(buffer, input_ids, ignore_index, write_grad=write_grad)
         if write_grad:
             if inplace:
                 torch.autograd.graph.increment_version(logits)
             ctx.grad_buffer = buffer
+            ctx.workspace = ws
             ctx.input_ids = input_ids
             ctx.ignore_index = ignore_index
         return loss
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, grad_loss: Tensor):  # type: ignore[override]
-        grad = ctx.grad_buffer
-        ops.cross_entropy_shifted_scale_grad(grad, ctx.input_ids, grad_loss, ctx.ignore_index)
-        del ctx.grad_buffer
+        grad = getattr(ctx, "grad_buffer", None)
+        if grad is None:
+            raise RuntimeError(_REPEATED_BACKWARD)
+        ops.cross_entropy_shifted_scale_grad(grad, ctx.input_ids, grad_loss, ctx.ignore_index,
+                                             ctx.workspace)
+        ctx.grad_buffer = None
         return grad, None, None, None
 
 
@@ -96,18 +122,25 @@ def _check_targets(targets: Tensor, vocab: int, ignore_index: int) -> None:
             raise TritonCrossEntropyUnavailable("HIP cross-entropy targets are out of range.")
 
 
-def _validate(logits: Tensor, targets: Tensor, ignore_index: int, shift: bool) -> None:
+def _validate(logits: Tensor, targets: Tensor, ignore_index: int, shift: bool,
+              grad_in_place: bool) -> None:
     require_hip(TritonCrossEntropyUnavailable, "cross-entropy", logits, targets)
     if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         raise TritonCrossEntropyUnavailable("HIP cross-entropy supports float logits only.")
     try:
         if shift:
-            ops._shifted_desc(logits, targets)
+            b, s, bs, ss, v, _, _ = ops._shifted_desc(logits, targets)
+            rows = [(b, bs), (s, ss)]
         else:
-            outer, inner, _, _, _ = ops.ce_rows(logits)
+            outer, inner, os_, is_, v = ops.ce_rows(logits)
             ops.ce_target_strides(targets, outer, inner)
+            rows = [(outer, os_), (inner, is_)]
     except ValueError as error:
         raise TritonCrossEntropyUnavailable(f"HIP cross-entropy: {error}.") from error
+    if grad_in_place and not ops.rows_disjoint(rows, v):
+        raise TritonCrossEntropyUnavailable(
+            "HIP cross-entropy: logits rows overlap in memory, so the gradient cannot be "
+            "written into them; pass inplace=False.")
     if shift:
         _check_targets(targets[:, 1:], logits.size(2), ignore_index)
     else:
@@ -132,17 +165,25 @@ def triton_cross_entropy(
     PICOTRON_HIP_CE_CHECK=1 to raise instead, at the cost of a host sync).
     """
 
-    _validate(logits, targets, ignore_index, shift)
+    grad_in_place = bool(inplace) and logits.requires_grad and torch.is_grad_enabled()
+    _validate(logits, targets, ignore_index, shift, grad_in_place)
     fn = _FusedShiftedCrossEntropy if shift else _FusedCrossEntropy
     return fn.apply(logits, targets, int(ignore_index), bool(inplace))
 
 
 class CrossEntropyWithFallback:
     """Run the fused cross-entropy when enabled, else (or on failure) ``F.cross_entropy``
-    (reference cross_entropy.py:90-109)."""
+    (reference cross_entropy.py:90-109).
 
-    def __init__(self, *, use_triton: bool = False) -> None:
+    Like ``F.cross_entropy`` it leaves its input alone by default: the fused path then
+    writes the gradient into a copy of the logits.  ``inplace=True`` writes it into the
+    logits themselves (one read and one write of the logits in all), for callers that do not
+    read the logits after the loss -- the train loop (train_loop.py:136-160) is one: its
+    logits feed only the loss."""
+
+    def __init__(self, *, use_triton: bool = False, inplace: bool = False) -> None:
         self.use_triton = use_triton
+        self.inplace = inplace
         self._fallback_warned = False
 
     def __call__(self, logits: Tensor, targets: Tensor, *, shift: bool = False) -> Tensor:
@@ -152,7 +193,7 @@ class CrossEntropyWithFallback:
 
         if self.use_triton:
             try:
-                return triton_cross_entropy(logits, targets, shift=shift)
+                return triton_cross_entropy(logits, targets, shift=shift, inplace=self.inplace)
             except Exception as error:
                 if not self._fallback_warned:
                     warnings.warn(

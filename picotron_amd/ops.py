@@ -327,6 +327,19 @@ def ce_rows(logits: Tensor) -> tuple[int, int, int, int, int]:
     raise ValueError("cross-entropy logits must be (N, C) or (N, C, d)")
 
 
+def rows_disjoint(sizes_strides: list[tuple[int, int]], row_len: int) -> bool:
+    """True if rows of ``row_len`` contiguous elements, one per index of the given
+    (size, stride) dimensions, never share an element (sufficient test: each stride, in
+    increasing order, clears the extent spanned by the dimensions below it)."""
+
+    extent = row_len  # elements spanned by one index of every dimension seen so far
+    for stride, size in sorted((abs(st), sz) for sz, st in sizes_strides if sz > 1):
+        if stride < extent:
+            return False
+        extent += stride * (size - 1)
+    return True
+
+
 def ce_target_strides(targets: Tensor, outer: int, inner: int) -> tuple[int, int]:
     if targets.dtype != torch.long:
         raise ValueError("cross-entropy targets must be int64")
@@ -352,6 +365,9 @@ def cross_entropy(
     device = _check_cuda(logits, targets)
     outer, inner, os_, is_, vocab = ce_rows(logits)
     tos, tis = ce_target_strides(targets, outer, inner)
+    if write_grad and not rows_disjoint([(outer, os_), (inner, is_)], vocab):
+        raise ValueError("cross-entropy logits rows overlap in memory; the gradient cannot be "
+                         "written into them")
     rows = outer * inner
     ws_bytes = _lib.lib().pt_cross_entropy_workspace_bytes(rows)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
@@ -372,9 +388,13 @@ def cross_entropy_status(ws: Tensor) -> int:
 
 
 def cross_entropy_scale_grad(
-    dlogits: Tensor, targets: Tensor, grad_output: Tensor, ignore_index: int = -100
+    dlogits: Tensor, targets: Tensor, grad_output: Tensor, ignore_index: int = -100,
+    workspace: Tensor | None = None,
 ) -> None:
-    """dlogits *= grad_output in place (skipped on device when grad_output == 1)."""
+    """dlogits *= grad_output in place (skipped on device when grad_output == 1).  For fp16
+    the rows hold (softmax - onehot) * 2^15 * q / n_valid (q: the largest power of two not
+    above n_valid) and ``workspace`` (the forward's) supplies n_valid:
+    dlogits *= grad_output * 2^-15 / q."""
 
     device = _check_cuda(dlogits, targets, grad_output)
     outer, inner, os_, is_, vocab = ce_rows(dlogits)
@@ -383,7 +403,8 @@ def cross_entropy_scale_grad(
     _lib.call(
         "pt_cross_entropy_scale_grad",
         dlogits.data_ptr(), outer, inner, os_, is_, vocab, targets.data_ptr(), tos, tis,
-        int(ignore_index), go.data_ptr(), dtype_code(dlogits.dtype), _stream(device),
+        int(ignore_index), go.data_ptr(), _ptr(workspace), dtype_code(dlogits.dtype),
+        _stream(device),
     )
 
 
@@ -411,6 +432,9 @@ def cross_entropy_shifted(
 
     device = _check_cuda(logits, input_ids)
     b, s, bs, ss, v, ibs, iss = _shifted_desc(logits, input_ids)
+    if write_grad and not rows_disjoint([(b, bs), (s, ss)], v):
+        raise ValueError("cross-entropy logits rows overlap in memory; the gradient cannot be "
+                         "written into them")
     ws_bytes = _lib.lib().pt_cross_entropy_workspace_bytes(b * s)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     loss = torch.empty((), dtype=torch.float32, device=device)
@@ -424,9 +448,11 @@ def cross_entropy_shifted(
 
 
 def cross_entropy_shifted_scale_grad(
-    dlogits: Tensor, input_ids: Tensor, grad_output: Tensor, ignore_index: int = -100
+    dlogits: Tensor, input_ids: Tensor, grad_output: Tensor, ignore_index: int = -100,
+    workspace: Tensor | None = None,
 ) -> None:
-    """dlogits *= grad_output in place for a gradient from :func:`cross_entropy_shifted`."""
+    """dlogits *= grad_output in place for a gradient from :func:`cross_entropy_shifted`
+    (fp16: as :func:`cross_entropy_scale_grad`, with the forward's ``workspace``)."""
 
     device = _check_cuda(dlogits, input_ids, grad_output)
     b, s, bs, ss, v, ibs, iss = _shifted_desc(dlogits, input_ids)
@@ -434,7 +460,7 @@ def cross_entropy_shifted_scale_grad(
     _lib.call(
         "pt_cross_entropy_shifted_scale_grad",
         dlogits.data_ptr(), b, s, bs, ss, v, input_ids.data_ptr(), ibs, iss, int(ignore_index),
-        go.data_ptr(), dtype_code(dlogits.dtype), _stream(device),
+        go.data_ptr(), _ptr(workspace), dtype_code(dlogits.dtype), _stream(device),
     )
 
 

@@ -106,8 +106,8 @@ def test_whole_training_step_replays_in_a_graph(gpu):
     graph_model, eager_model = _model(gpu), _model(gpu)
     graph_opt = torch.optim.AdamW(graph_model.parameters(), capturable=True, **HP)
     eager_opt = torch.optim.AdamW(eager_model.parameters(), capturable=True, **HP)
-    graph_loss_fn = CrossEntropyWithFallback(use_triton=True)
-    eager_loss_fn = CrossEntropyWithFallback(use_triton=True)
+    graph_loss_fn = CrossEntropyWithFallback(use_triton=True, inplace=True)
+    eager_loss_fn = CrossEntropyWithFallback(use_triton=True, inplace=True)
     x_static, ids_static = _inputs(gpu, 0)
 
     side = torch.cuda.Stream()

@@ -7,6 +7,7 @@ import math
 import numpy as np
 import pytest
 import torch
+from torch.nn import functional as F
 
 from conftest import GOLDEN
 from gpu_util import from_npz, randn
@@ -37,6 +38,9 @@ def _check(logits, targets, dtype):
     loss2, ws = ops.cross_entropy(buf, targets, write_grad=True)
     assert loss2.item() == loss.item()  # the loss does not depend on writing the gradient
     assert ops.cross_entropy_status(ws) == 0
+    # the backward for a grad_output of 1: nothing for fp32 / bf16; fp16 rows hold
+    # 2^15 (softmax - onehot) until it divides by n_valid * 2^15
+    ops.cross_entropy_scale_grad(buf, targets, torch.ones((), device=logits.device), workspace=ws)
     _grad_close(buf, ref_grad, n_valid, dtype)
     return buf
 
@@ -313,7 +317,11 @@ def test_scale_grad_is_the_elementwise_product(gpu, dtype, vocab, offset):
     targets[[2, 7]] = -100
     before = buf.clone()
     outside = base[:, :offset].clone()
-    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu))
+    # fp16 multiplies by grad_output * 2^-15 / q, q the largest power of two not above
+    # n_valid: a workspace whose n_valid is 2^-15 makes that exactly grad_output
+    ws = torch.zeros(4, dtype=torch.float32, device=gpu)
+    ws[0] = 2.0 ** -15
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu), workspace=ws)
     kept = (targets != -100).unsqueeze(1)
     want = torch.where(kept, (before.float() * 0.37).to(dtype), before)
     assert torch.equal(buf, want)
@@ -331,9 +339,109 @@ def test_scale_grad(gpu, dtype, vocab):
     targets[4] = -100
     _, ref_grad = o_ce.forward_backward(logits, targets)
     buf = logits.clone()
-    ops.cross_entropy(buf, targets, write_grad=True)
-    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu))
+    _, ws = ops.cross_entropy(buf, targets, write_grad=True)
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(0.37, device=gpu), workspace=ws)
     _grad_close(buf, 0.37 * ref_grad, rows - 1, dtype)
-    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(float("nan"), device=gpu))
+    ops.cross_entropy_scale_grad(buf, targets, torch.tensor(float("nan"), device=gpu), workspace=ws)
     assert bool((buf[4] == 0).all())
     assert bool(torch.isnan(buf[targets != -100]).all())
+
+
+@pytest.mark.parametrize("shift", [False, True])
+def test_fp16_gradients_at_training_scale(gpu, shift):
+    """fp16 logits at the training shape with a GradScaler-sized loss gradient (65536).
+
+    softmax / n_valid (about 1e-10 here) lies far below fp16's smallest subnormal, so a
+    gradient stored before the scale is known would be all zeros: at least 99% of the entries
+    of the rows that have a target must be nonzero.  Bounds are relative, with an absolute floor of two fp16 subnormal steps
+    (independent of the row count), against two references:
+    - F.cross_entropy on the fp32 upcast, its gradient rounded to fp16 once (within half an
+      fp16 unit of the exact gradient): 1.5e-3 relative;
+    - the reference's own call, F.cross_entropy under fp16 autocast: its backward deviates from
+      the exact gradient by up to 0.44% on this build (measured; an fp32 computation rounded once
+      deviates by 0.05%), so 6e-3 relative.
+    """
+
+    from picotron_amd.nn.triton_kernels import triton_cross_entropy
+
+    vocab, scale = 128256, 65536.0
+    shape = (2, 1025, vocab) if shift else (8192, vocab)
+    print(f"fp16 ce shape {shape} shift {shift}", flush=True)
+    logits = randn(shape, torch.float16, gpu, 91, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(92)
+    if shift:
+        targets = torch.randint(0, vocab, shape[:2], generator=g, device=gpu)
+        targets[0, 7:300] = -100
+    else:
+        targets = torch.randint(0, vocab, shape[:1], generator=g, device=gpu)
+        targets[torch.randperm(shape[0], generator=g, device=gpu)[:410]] = -100
+
+    def reference(cast_fp32: bool):
+        leaf = logits.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.float16, enabled=not cast_fp32):
+            t = leaf.float() if cast_fp32 else leaf
+            if shift:
+                loss = F.cross_entropy(t[:, :-1, :].transpose(1, 2), targets[:, 1:])
+            else:
+                loss = F.cross_entropy(t, targets)
+        (loss * scale).backward()
+        return loss.detach(), leaf.grad
+
+    x = logits.clone().requires_grad_(True)
+    loss = triton_cross_entropy(x * 1, targets, shift=shift)
+    (loss * scale).backward()
+    got = x.grad.float()
+    assert x.grad.dtype == torch.float16
+    for cast_fp32, rtol in ((True, 1.5e-3), (False, 6e-3)):
+        ref_loss, ref = reference(cast_fp32)
+        assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+        ref = ref.float()
+        excess = (got - ref).abs() - (rtol * ref.abs() + 2.0 ** -23)
+        assert float(excess.max()) <= 0, f"fp32-upcast reference {cast_fp32}: max excess {float(excess.max())}"
+        if cast_fp32:  # over the rows that have a target (ignored rows are zero)
+            kept = (targets[:, 1:] if shift else targets) != -100
+            rows_got = (got[:, :-1] if shift else got)[kept]
+            rows_ref = (ref[:, :-1] if shift else ref)[kept]
+            nonzero = float((rows_got != 0).float().mean())
+            assert nonzero > 0.99, nonzero
+            assert abs(nonzero - float((rows_ref != 0).float().mean())) < 1e-3
+            del rows_got, rows_ref
+        del ref, excess
+
+
+def test_repeated_backward_raises_clearly(gpu):
+    from picotron_amd.nn.triton_kernels import triton_cross_entropy
+
+    logits = randn((4, 300), torch.bfloat16, gpu, 93, 2.0)
+    targets = torch.tensor([1, 2, -100, 299], device=gpu)
+    x = logits.clone().requires_grad_(True)
+    loss = triton_cross_entropy(x * 1, targets)
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="consumed by an earlier backward"):
+        loss.backward()
+
+
+def test_overlapping_rows_are_never_written_in_place(gpu):
+    from picotron_amd.nn.triton_kernels import (
+        CrossEntropyWithFallback,
+        TritonCrossEntropyUnavailable,
+        triton_cross_entropy,
+    )
+
+    row = randn((1, 500), torch.bfloat16, gpu, 94, 2.0).requires_grad_(True)
+    expanded = row.expand(6, 500)  # six rows on one row of memory
+    targets = torch.tensor([0, 1, 2, 3, -100, 499], device=gpu)
+    with pytest.raises(TritonCrossEntropyUnavailable, match="overlap"):
+        triton_cross_entropy(expanded, targets)
+    # out of place it runs, and matches the oracle on the materialised rows
+    ref_loss, ref_grad = o_ce.forward_backward(expanded.detach().contiguous(), targets)
+    loss = triton_cross_entropy(expanded, targets, inplace=False)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    loss.backward()
+    _grad_close(row.grad, ref_grad.sum(0, keepdim=True), 5, torch.bfloat16)
+    # the drop-in keeps its input by default, like F.cross_entropy
+    logits = randn((5, 700), torch.bfloat16, gpu, 95, 2.0)
+    y = logits.clone().requires_grad_(True) * 1
+    before = y.detach().clone()
+    CrossEntropyWithFallback(use_triton=True)(y, torch.tensor([0, 5, 9, -100, 699], device=gpu)).backward()
+    assert torch.equal(y.detach(), before)

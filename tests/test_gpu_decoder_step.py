@@ -91,7 +91,7 @@ def _models(gpu):
 def _step(model, fused: bool, ids, *, eps: float, autocast: bool):
     optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, betas=(0.9, 0.95), eps=eps,
                                   weight_decay=0.1, foreach=False)
-    loss_fn = CrossEntropyWithFallback(use_triton=fused)
+    loss_fn = CrossEntropyWithFallback(use_triton=fused, inplace=True)
     stepper = AdamWStepWithFallback(use_triton=fused)
     with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
         logits = model(ids)
@@ -146,7 +146,7 @@ def test_fp16_autocast_with_loss_scaling_tracks_the_fallback_model(gpu):
     scale = 4096.0
 
     def scaled_step(model, use_fused):
-        loss_fn = CrossEntropyWithFallback(use_triton=use_fused)
+        loss_fn = CrossEntropyWithFallback(use_triton=use_fused, inplace=True)
         with torch.autocast("cuda", dtype=torch.float16):
             logits = model(ids)
             loss = loss_fn(logits, ids, shift=True)

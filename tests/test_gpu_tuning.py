@@ -42,8 +42,8 @@ _SCRIPT = textwrap.dedent("""
     add(*ops.rope(q, ang.cos(), ang.sin(), layout="rotate_half", x1=k))
     logits = randn(300, 50257) * 2
     targets = torch.randint(0, 50257, (300,), generator=gen, device=dev)
-    loss, _ = ops.cross_entropy(logits, targets, write_grad=True)
-    ops.cross_entropy_scale_grad(logits, targets, torch.tensor(0.37, device=dev))
+    loss, ws = ops.cross_entropy(logits, targets, write_grad=True)
+    ops.cross_entropy_scale_grad(logits, targets, torch.tensor(0.37, device=dev), workspace=ws)
     add(loss, logits)
     p = torch.nn.Parameter(randn(1 << 20, dtype=torch.float32))
     p.grad = randn(1 << 20, dtype=torch.float32)
