@@ -10,6 +10,7 @@ from picotron_amd.nn.triton_kernels.adamw import (
     TritonAdamWUnavailable,
     triton_adamw_step,
     triton_clip_grad_norm_and_step,
+    triton_grad_scaler_step,
     triton_unscale_and_check_,
     triton_unscale_clip_and_step,
     triton_zero_clip_grad_norm_,
@@ -60,6 +61,7 @@ __all__ = [
     "triton_adamw_step",
     "triton_apply_rotary_embedding_pair",
     "triton_clip_grad_norm_and_step",
+    "triton_grad_scaler_step",
     "triton_residual_rms_norm",
     "triton_unscale_and_check_",
     "triton_unscale_clip_and_step",

@@ -71,6 +71,29 @@ def _check_param(p: Tensor) -> None:
         raise _reject("non-contiguous parameters or gradients")
 
 
+def _check_state(state: dict, p: Tensor) -> None:
+    """An existing optimizer state (resumed from a checkpoint, or written by torch's own step)
+    must be what the kernel's raw pointers assume: fp32 contiguous moments of p's size on p's
+    device and a one-element step tensor.  ``Optimizer.load_state_dict`` does not check state
+    shapes, and torch's step would raise on a mismatch where the kernel would read and write
+    out of bounds."""
+
+    if len(state) == 0:
+        return
+    step = state.get("step")
+    if not isinstance(step, Tensor) or step.numel() != 1:
+        raise _reject("optimizer states whose step is not a one-element tensor")
+    for key in ("exp_avg", "exp_avg_sq"):
+        m = state.get(key)
+        if not isinstance(m, Tensor):
+            raise _reject(f"optimizer states without {key}")
+        if m.dtype != torch.float32 or m.device != p.device or m.is_sparse:
+            raise _reject(f"optimizer states whose {key} is not fp32 on the parameter's device")
+        if m.numel() != p.numel() or not m.is_contiguous():
+            raise _reject(f"optimizer states whose {key} does not match the parameter "
+                          f"({tuple(m.shape)} for {tuple(p.shape)}, or not contiguous)")
+
+
 _table_cache: dict[tuple, Tensor] = {}
 _TABLE_CACHE_SIZE = 16
 # Tables used while a stream is being captured into a graph: the graph's kernels read them
@@ -115,6 +138,7 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
         _check_group(group)
         params = [p for p in group["params"] if p.grad is not None]
         for p in params:
+            _check_state(optimizer.state.get(p, {}), p)
             _check_param(p)
             if device is None:
                 device = p.device
@@ -380,6 +404,69 @@ def triton_unscale_clip_and_step(
     return False
 
 
+def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float | None = None) -> bool:
+    """The train loop's single-GPU fp16 update, fused: ``grad_scaler.unscale_(optimizer)``,
+    ``torch.nn.utils.clip_grad_norm_(params, max_norm)`` (when ``max_norm`` is given),
+    ``grad_scaler.step(optimizer)`` and ``grad_scaler.update()`` (reference
+    src/picotron/training/train_loop.py:155-160, with the ``torch.amp.GradScaler`` created at
+    :285-296 for fp16 without ZeRO and ``_clip_gradients`` at :338-350).
+
+    One pass reads every gradient for the finite check, the norm of the unscaled gradients and
+    the combined multiplier ``inv_scale * clip_coef`` (``inv_scale`` is the scaler's
+    ``1 / scale`` computed as ``unscale_`` computes it, in double then rounded to fp32); one
+    host read of the finite flag, as ``grad_scaler.step`` makes; then the AdamW step applies the
+    multiplier as it reads each gradient and writes the unscaled, clipped gradient back.  When a
+    gradient is inf or NaN the step is skipped (no state is created or advanced), the gradients
+    are left unscaled as ``unscale_`` leaves them, and the scaler backs off exactly as torch's:
+    the flag is recorded in the scaler's per-optimizer state as ``unscale_`` records it, and
+    ``grad_scaler.update()`` consumes it.  Returns True when the step was skipped.
+
+    With a power-of-two scale (torch's defaults: 65536, growth 2, backoff 0.5) the unscaled
+    gradients are bitwise torch's; the clip coefficient follows torch's formula with the norm
+    summed in a different order (fp32 rounding of the last bits).
+    """
+
+    from torch.amp.grad_scaler import OptState
+
+    if not isinstance(grad_scaler, torch.amp.GradScaler):
+        raise _reject(f"{type(grad_scaler).__name__} (only torch.amp.GradScaler)")
+    if max_norm is not None and max_norm <= 0:
+        raise ValueError("max_norm must be positive.")
+    if not grad_scaler.is_enabled():
+        if max_norm is None:
+            triton_adamw_step(optimizer)
+        else:
+            triton_clip_grad_norm_and_step(optimizer, max_norm)
+        return False
+    scale, _ = grad_scaler._check_scale_growth_tracker("step")
+    state = grad_scaler._per_optimizer_states[id(optimizer)]
+    if state["stage"] is not OptState.READY:
+        raise _reject("a GradScaler that already unscaled or stepped this optimizer this iteration")
+    groups, device = _plan(optimizer)
+    if device is None:
+        raise _reject("an optimizer without gradients")
+    if scale.device != device:
+        raise _reject("a loss scale on another device than the gradients")
+    grads = [p.grad for _, params in groups for p in params]
+    table, blocks = _grad_table(grads, device)
+    # every check that can fail is done: from here on the call runs to the end
+    inv_scale = scale.double().reciprocal().float()
+    _, multiplier, found_inf = ops.grad_stats(
+        table, blocks, inv_scale, max_norm, ops.CLIP_CLAMP)
+    launches, created = _prepare(optimizer, groups, device)
+    skipped = bool(found_inf.item())
+    if skipped:
+        for p in created:  # a skipped step leaves no state behind
+            del optimizer.state[p]
+        ops.grad_scale(table, blocks, inv_scale)
+    else:
+        _launch(optimizer, groups, launches, multiplier, True)
+    state["found_inf_per_device"] = {device: found_inf.float()}
+    state["stage"] = OptState.STEPPED
+    grad_scaler.update()
+    return skipped
+
+
 class AdamWStepWithFallback:
     """Attempt the fused step when enabled, else (or on failure) ``optimizer.step()``
     (reference adamw.py:27-47)."""
@@ -411,3 +498,29 @@ class AdamWStepWithFallback:
             params = [p for group in optimizer.param_groups for p in group["params"]]
             torch.nn.utils.clip_grad_norm_(params, max_grad_norm)
         optimizer.step()
+
+    def step_with_grad_scaler(self, grad_scaler, optimizer: Optimizer,
+                              max_grad_norm: float | None = None) -> None:
+        """The train loop's fp16 update (reference src/picotron/training/train_loop.py:155-160):
+        ``grad_scaler.unscale_``, ``clip_grad_norm_`` when ``max_grad_norm`` is given,
+        ``grad_scaler.step`` and ``grad_scaler.update``; fused on the fast path
+        (:func:`triton_grad_scaler_step`), else exactly that torch sequence."""
+
+        if self.use_triton:
+            try:
+                triton_grad_scaler_step(grad_scaler, optimizer, max_grad_norm)
+                return
+            except Exception as error:
+                if not self._fallback_warned:
+                    warnings.warn(
+                        f"Triton AdamW unavailable; using PyTorch fallback: {error}",
+                        RuntimeWarning,
+                        stacklevel=2,
+                    )
+                    self._fallback_warned = True
+        grad_scaler.unscale_(optimizer)
+        if max_grad_norm is not None:
+            params = [p for group in optimizer.param_groups for p in group["params"]]
+            torch.nn.utils.clip_grad_norm_(params, max_grad_norm)
+        grad_scaler.step(optimizer)
+        grad_scaler.update()

@@ -317,3 +317,34 @@ def test_stepper_with_clipping_and_no_gradients(gpu):
     torch.nn.utils.clip_grad_norm_(ref, 1.0)
     torch.optim.AdamW(ref, foreach=False, **HP).step()
     close_fp32(fused[0].detach(), ref[0].detach())
+
+
+@pytest.mark.parametrize(
+    "bad",
+    ["short", "offloaded", "float64", "strided", "no_moment"],
+)
+def test_mismatched_resumed_state_is_refused_before_launch(gpu, bad):
+    """A state loaded from a checkpoint that does not match the parameter (short, on the CPU,
+    fp64, a strided view, missing a moment) is refused by the fused step with nothing
+    launched and nothing changed; torch's own step decides what happens then."""
+
+    p = torch.nn.Parameter(randn((5000,), torch.float32, gpu, 3))
+    p.grad = randn((5000,), torch.float32, gpu, 4)
+    opt = torch.optim.AdamW([p], **HP)
+    m = torch.zeros(5000, device=gpu)
+    states = {
+        "short": dict(exp_avg=torch.zeros(4096, device=gpu), exp_avg_sq=m.clone()),
+        "offloaded": dict(exp_avg=torch.zeros(5000), exp_avg_sq=m.clone()),
+        "float64": dict(exp_avg=torch.zeros(5000, dtype=torch.float64, device=gpu), exp_avg_sq=m.clone()),
+        "strided": dict(exp_avg=torch.zeros(10000, device=gpu)[::2], exp_avg_sq=m.clone()),
+        "no_moment": dict(exp_avg_sq=m.clone()),
+    }
+    opt.state[p] = dict(step=torch.tensor(2.0), **states[bad])
+    before = p.detach().clone()
+    from picotron_amd.nn.triton_kernels import TritonAdamWUnavailable
+
+    with pytest.raises(TritonAdamWUnavailable):
+        triton_adamw_step(opt)
+    torch.cuda.synchronize()
+    assert torch.equal(p.detach(), before)
+    assert float(opt.state[p]["step"]) == 2.0

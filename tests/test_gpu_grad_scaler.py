@@ -1,0 +1,137 @@
+"""The train loop's single-GPU fp16 update (torch.amp.GradScaler: unscale_, clip_grad_norm_,
+step, update; reference src/picotron/training/train_loop.py:155-160) fused, against the same
+torch sequence step by step: parameters, moments, step counts, the scaler's scale and growth
+tracker, and the gradients it leaves, over steps that grow the scale and steps that overflow."""
+
+from __future__ import annotations
+
+import warnings
+
+import pytest
+import torch
+
+from gpu_util import close_fp32, randn
+from picotron_amd.nn.triton_kernels import (
+    AdamWStepWithFallback,
+    TritonAdamWUnavailable,
+    triton_grad_scaler_step,
+)
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+SIZES = [1, 3, 4095, 4096, 4097, 70_000, 1 << 20]
+
+
+def _setup(gpu, seed):
+    fused = [torch.nn.Parameter(randn((n,), torch.float32, gpu, seed + n, 0.02)) for n in SIZES]
+    fused.append(torch.nn.Parameter(torch.ones(5, device=gpu)))  # never gets a gradient
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in fused]
+    opt_f = torch.optim.AdamW(fused, **HP)
+    opt_r = torch.optim.AdamW(ref, foreach=False, **HP)
+    scalers = []
+    for _ in range(2):
+        sc = torch.amp.GradScaler("cuda", init_scale=2.0 ** 16, growth_interval=2)
+        sc.scale(torch.ones((), device=gpu))  # creates the scale tensor, as scale(loss) does
+        scalers.append(sc)
+    return fused, ref, opt_f, opt_r, scalers[0], scalers[1]
+
+
+def _set_grads(fused, ref, gpu, seed, scale, bad=None):
+    for i, (a, b) in enumerate(zip(fused[:-1], ref[:-1])):
+        g = randn(a.shape, torch.float32, gpu, seed + i, 1e-3 * scale)
+        if bad is not None and i == 4:
+            g[4096] = bad  # the second block of one tensor
+        a.grad, b.grad = g, g.clone()
+
+
+def _reference_step(sc, opt, params, max_norm):
+    sc.unscale_(opt)
+    if max_norm is not None:
+        torch.nn.utils.clip_grad_norm_(params, max_norm)
+    sc.step(opt)
+    sc.update()
+
+
+def _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too):
+    assert sc_f.get_scale() == sc_r.get_scale()
+    assert sc_f._growth_tracker.item() == sc_r._growth_tracker.item()
+    for a, b in zip(fused, ref):
+        sa, sb = opt_f.state.get(a, {}), opt_r.state.get(b, {})
+        assert set(sa) == set(sb)
+        close_fp32(a.detach(), b.detach())
+        if sb:
+            assert sa["step"].item() == sb["step"].item()
+            close_fp32(sa["exp_avg"], sb["exp_avg"])
+            close_fp32(sa["exp_avg_sq"], sb["exp_avg_sq"])
+        if grads_too and b.grad is not None:
+            if torch.isfinite(b.grad).all():
+                close_fp32(a.grad, b.grad)
+            else:  # an overflow step without clipping: both are g * (1 / scale), exactly
+                assert torch.equal(a.grad.nan_to_num(), b.grad.nan_to_num())
+
+
+# (step, bad value): an overflow on the first step (no state may be created), one after the
+# scale has grown, and a NaN right after a backoff
+OVERFLOWS = {0: float("inf"), 3: float("-inf"), 4: float("nan")}
+
+
+@pytest.mark.parametrize("max_norm", [None, 1e-3, 1e4])
+def test_fused_grad_scaler_step_matches_torch_sequence(gpu, max_norm):
+    fused, ref, opt_f, opt_r, sc_f, sc_r = _setup(gpu, 5)
+    for step in range(8):
+        scale = sc_r.get_scale()
+        bad = OVERFLOWS.get(step)
+        print(f"grad scaler step {step} scale {scale} bad {bad} max_norm {max_norm}", flush=True)
+        _set_grads(fused, ref, gpu, 100 * step, scale, bad)
+        _reference_step(sc_r, opt_r, ref, max_norm)
+        skipped = triton_grad_scaler_step(sc_f, opt_f, max_norm)
+        assert skipped == (bad is not None)
+        # after a skipped step torch's clip has run on non-finite gradients (0 or NaN
+        # everywhere); the fused path leaves them unscaled, as unscale_ does
+        _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=bad is None or max_norm is None)
+    # the scale grew twice and backed off three times: 2^16 * 2^2 / 2^3
+    assert sc_f.get_scale() == 2.0 ** 15
+
+
+def test_unclipped_gradients_are_torch_bits(gpu):
+    """With a power-of-two scale and no clipping the unscaled gradients are bitwise torch's."""
+
+    fused, ref, opt_f, opt_r, sc_f, sc_r = _setup(gpu, 6)
+    _set_grads(fused, ref, gpu, 7, sc_r.get_scale())
+    _reference_step(sc_r, opt_r, ref, None)
+    triton_grad_scaler_step(sc_f, opt_f, None)
+    for a, b in zip(fused[:-1], ref[:-1]):
+        assert torch.equal(a.grad, b.grad)
+
+
+def test_fallback_class_uses_the_fused_path_without_warning(gpu):
+    fused, ref, opt_f, opt_r, sc_f, sc_r = _setup(gpu, 7)
+    stepper = AdamWStepWithFallback(use_triton=True)
+    for step in range(3):
+        scale = sc_r.get_scale()
+        _set_grads(fused, ref, gpu, 300 + step, scale, float("inf") if step == 1 else None)
+        _reference_step(sc_r, opt_r, ref, 1.0)
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")
+            stepper.step_with_grad_scaler(sc_f, opt_f, 1.0)
+        _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=step != 1)
+
+
+def test_already_unscaled_optimizer_is_rejected_untouched(gpu):
+    """A caller that ran unscale_ itself is refused before anything changes (the fused path
+    would unscale twice), so torch's own step() and update() can follow."""
+
+    fused, ref, opt_f, opt_r, sc_f, sc_r = _setup(gpu, 8)
+    _set_grads(fused, ref, gpu, 9, sc_r.get_scale())
+    sc_f.unscale_(opt_f)
+    grads = [p.grad.clone() for p in fused[:-1]]
+    with pytest.raises(TritonAdamWUnavailable, match="already unscaled"):
+        triton_grad_scaler_step(sc_f, opt_f, None)
+    for p, g in zip(fused[:-1], grads):
+        assert torch.equal(p.grad, g)
+    assert not opt_f.state
+    sc_f.step(opt_f)
+    sc_f.update()
+    _reference_step(sc_r, opt_r, ref, None)
+    _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=True)

@@ -28,6 +28,7 @@ from picotron_amd.nn.triton_kernels import (
     rms_norm_with_pytorch_forward,
     swiglu_with_pytorch_forward,
     triton_adamw_step,
+    triton_grad_scaler_step,
     triton_apply_rotary_embedding,
     triton_causal_attention,
     triton_cross_entropy,
@@ -200,6 +201,62 @@ def test_adamw_clip_fallback_is_clip_grad_norm_then_step():
     for p, q in zip(ref_params, params):
         torch.testing.assert_close(q, p, rtol=0, atol=0)
         torch.testing.assert_close(q.grad, p.grad, rtol=0, atol=0)
+
+
+def test_grad_scaler_fallback_is_the_train_loop_fp16_sequence():
+    """On CPU the fused GradScaler update refuses and the fallback runs the reference
+    sequence (train_loop.py:155-160): unscale_, clip_grad_norm_, step, update."""
+
+    torch.manual_seed(5)
+    ref_params = [torch.nn.Parameter(torch.randn(5)), torch.nn.Parameter(torch.randn(3, 2))]
+    params = [torch.nn.Parameter(p.detach().clone()) for p in ref_params]
+    scalers = [torch.amp.GradScaler("cpu", init_scale=1024.0, growth_interval=1) for _ in range(2)]
+    for sc in scalers:
+        sc.scale(torch.ones(()))
+    ref_opt, opt = AdamW(ref_params, lr=0.01, weight_decay=0.1), AdamW(params, lr=0.01, weight_decay=0.1)
+    stepper = AdamWStepWithFallback(use_triton=True)
+    for step in range(2):
+        for p, q in zip(ref_params, params):
+            p.grad = torch.randn_like(p) * 4 * scalers[0].get_scale()
+            q.grad = p.grad.clone()
+        scalers[0].unscale_(ref_opt)
+        torch.nn.utils.clip_grad_norm_(ref_params, 1.0)
+        scalers[0].step(ref_opt)
+        scalers[0].update()
+        if step == 0:
+            with pytest.warns(RuntimeWarning, match="Triton AdamW unavailable"):
+                stepper.step_with_grad_scaler(scalers[1], opt, 1.0)
+        else:  # warned once
+            stepper.step_with_grad_scaler(scalers[1], opt, 1.0)
+        for p, q in zip(ref_params, params):
+            torch.testing.assert_close(q, p, rtol=0, atol=0)
+            torch.testing.assert_close(q.grad, p.grad, rtol=0, atol=0)
+        assert scalers[1].get_scale() == scalers[0].get_scale() == 1024.0 * 2 ** (step + 1)
+    with pytest.raises(RuntimeError, match="not implemented"):
+        triton_grad_scaler_step(scalers[1], opt, 1.0)
+
+
+def test_adamw_rejects_mismatched_resumed_state_before_anything_runs():
+    """A resumed state whose moments do not match the parameter (load_state_dict does not
+    check shapes) is refused by the fused step before any pointer is taken; the fallback then
+    runs torch's step, which reports the mismatch itself."""
+
+    p = torch.nn.Parameter(torch.randn(6))
+    p.grad = torch.randn(6)
+    opt = AdamW([p], lr=0.01)
+    opt.state[p] = {"step": torch.tensor(3.0), "exp_avg": torch.zeros(4), "exp_avg_sq": torch.zeros(6)}
+    with pytest.raises(TritonAdamWUnavailable, match="exp_avg does not match"):
+        triton_adamw_step(opt)
+    stepper = AdamWStepWithFallback(use_triton=True)
+    with pytest.warns(RuntimeWarning, match="Triton AdamW unavailable"):
+        with pytest.raises(RuntimeError):
+            stepper.step(opt)
+    opt.state[p] = {"step": torch.tensor(3.0), "exp_avg": torch.zeros(12)[::2], "exp_avg_sq": torch.zeros(6)}
+    with pytest.raises(TritonAdamWUnavailable, match="not contiguous"):
+        triton_adamw_step(opt)
+    opt.state[p] = {"step": 3.0, "exp_avg": torch.zeros(6), "exp_avg_sq": torch.zeros(6)}
+    with pytest.raises(TritonAdamWUnavailable, match="one-element tensor"):
+        triton_adamw_step(opt)
 
 
 def test_adamw_fallback_matches_known_single_step_update():
