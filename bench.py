@@ -1,14 +1,17 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|zero_step|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|zero_step|fp16_step|modules|copy]
 
-Default workload (the headline metric): RMSNorm forward + backward, bf16, 16384 tokens
-(8 x 2048) x 4096, eps 1e-5, bf16 weight, rstd kept in fp32.  One step runs the forward of
-``--layers`` independent activations (as the norms of consecutive decoder layers) and then
-their backward in reverse order, so no input is cache-resident when it is read (each
-activation is 134 MB; the working set of a step is ``layers`` x 537 MB against a 256 MB
-Infinity Cache).  Inputs are synthetic (seeded N(0,1), weight 1 + 0.02 N(0,1)) and
-resident in HBM before timing.
+Default workload (the headline metric, "RMSNorm/SwiGLU fwd+bwd"): ``--layers`` decoder layers
+(default 4), each with its own activations: the RMSNorm forward of a bf16 [16384 tokens
+(8 x 2048), 4096] activation (eps 1e-5, bf16 weight, rstd kept in fp32) and the SwiGLU
+forward of bf16 [16384, 14336] gate/up, then the backwards in reverse layer order.  A layer's
+working set (3.4 GB) is far above the 256 MB Infinity Cache, so no input is cache-resident
+when it is read.  Inputs are synthetic (seeded N(0,1), weight 1 + 0.02 N(0,1)) and resident
+in HBM before timing.  The line also carries each op timed alone (``config.ops``: the
+per-op GB/s and % of peak the >=75% target is stated for), every kernel's event timing
+(``roofline.per_kernel``) and compact figures for the RoPE, cross-entropy and AdamW
+configurations (``config.other_configs``).
 
 Prints ONE JSON line: value = algorithmic bytes of the step / wall time of the step
 (decimal GB/s) over K timed steps bracketed by device synchronisations, with a
@@ -411,6 +414,134 @@ class SwiGLUWorkload(Workload):
                    f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
+
+
+class HeadlineWorkload(Workload):
+    """The headline pair as consecutive decoder layers run it: per layer the RMSNorm forward of
+    a [16384, 4096] bf16 activation, then the SwiGLU forward of [16384, 14336] bf16 gate/up;
+    then the backwards in reverse layer order (SwiGLU, then RMSNorm).  Every layer has its own
+    activations (each layer's set is 3.4 GB against a 256 MB Infinity Cache), so no input is
+    cache-resident when it is read.  Reference paths: src/picotron/nn/triton_kernels/
+    rmsnorm.py:87-134 and swiglu.py:56-81, behind picotron_decoder.py:32-46 and
+    feedforward.py:26-43."""
+
+    name = "headline"
+    metric = HEADLINE_METRIC
+
+    def __init__(self, layers: int) -> None:
+        self.layers = layers
+        self.rms = RMSNormWorkload(layers)
+        self.swiglu = SwiGLUWorkload(layers)
+        n = self.swiglu.n
+        self.bytes_per_step = self.rms.bytes_per_step + self.swiglu.bytes_per_step
+        self.tokens_per_step = layers * RMSNormWorkload.rows
+        self.kinds = {
+            "rmsnorm_forward": dict(op="rmsnorm", kernel="rmsnorm_fwd_kernel",
+                                    bytes=self.rms.fwd_bytes, calls=self.rms._fwd),
+            "rmsnorm_backward": dict(op="rmsnorm", kernel="rmsnorm_bwd_kernel + rmsnorm_dw_finish_kernel",
+                                     bytes=self.rms.bwd_bytes, calls=self.rms._bwd),
+            "swiglu_forward": dict(op="swiglu", kernel="swiglu_fwd_kernel", bytes=3 * n * 2,
+                                   calls=self.swiglu._fwd),
+            "swiglu_backward": dict(op="swiglu", kernel="swiglu_bwd_kernel", bytes=5 * n * 2,
+                                    calls=self.swiglu._bwd),
+        }
+        self.timed_kinds = {kind: layers for kind in self.kinds}
+        self.description = (
+            f"RMSNorm fwd+bwd bf16 [16384 tokens (8x2048), 4096] (eps 1e-5, bf16 weight, fp32 rstd) and "
+            f"SwiGLU fwd+bwd bf16 gate/up [16384, 14336]; step = {layers} decoder layers: per layer the "
+            f"norm forward then the SwiGLU forward, then the backwards in reverse layer order"
+        )
+
+    def _launch(self, kind: str, i: int, events) -> None:
+        fn, args = self.kinds[kind]["calls"][i]
+        if events is not None:
+            start, end = events[kind].pop()
+            start.record()
+        rc = fn(*args)
+        if events is not None:
+            end.record()
+        if rc:
+            _lib.check(fn.__name__, rc)
+
+    def step(self, events):
+        for i in range(self.layers):
+            self._launch("rmsnorm_forward", i, events)
+            self._launch("swiglu_forward", i, events)
+        for i in reversed(range(self.layers)):
+            self._launch("swiglu_backward", i, events)
+            self._launch("rmsnorm_backward", i, events)
+
+    def extra(self, steps: int) -> dict:
+        """Each op alone over the same buffers (its own fwd+bwd step, host clock: the per-op
+        figures the >=75% target is stated for), the norm's forward against a plain copy of
+        the same bytes, and compact figures for the other three configurations."""
+
+        ops_out = {}
+        for op, wl, shape in (("rmsnorm", self.rms, [16384, 4096]), ("swiglu", self.swiglu, [16384, 14336])):
+            sec = _host_time(wl.step, steps)
+            gbps = wl.bytes_per_step / sec / 1e9
+            ops_out[op] = {
+                "shape": shape,
+                "layers_per_step": self.layers,
+                "algorithmic_bytes_per_step": wl.bytes_per_step,
+                "ms_per_step": round(sec * 1e3, 4),
+                "us_per_layer_fwd_bwd": round(sec * 1e6 / self.layers, 2),
+                "gbs": round(gbps, 1),
+                "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+                "tokens_per_s": round(wl.tokens_per_step / sec, 1),
+            }
+        ops_out["rmsnorm"].update(self.rms.extra(steps))
+        return {"ops": ops_out, "other_configs": _other_configs(steps)}
+
+    def cpu_baseline(self) -> dict:
+        rms, swiglu = self.rms.cpu_baseline(), self.swiglu.cpu_baseline()
+        # value is in GB/s: bytes of one call = value * 1e9 * seconds per call
+        nbytes = 1e9 * (rms["value"] * rms["seconds_per_call"] + swiglu["value"] * swiglu["seconds_per_call"])
+        sec = rms["seconds_per_call"] + swiglu["seconds_per_call"]
+        return dict(
+            value=nbytes / sec / 1e9, unit="GB/s", cores=rms["cores"], kind="port",
+            sample=f"one layer of each op: RMSNorm [{self.rms.rows}, {self.rms.cols}] and SwiGLU "
+                   f"[{self.swiglu.rows}, {self.swiglu.cols}] fwd+bwd through the reference PyTorch fallbacks "
+                   f"(rmsnorm.py:56-60,113-134; F.silu*up and swiglu.py:75-81) on bf16 CPU tensors; value = "
+                   f"bytes of both / time of both; each the median of ~{CPU_TARGET_S:.0f} s of calls after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=self.rms.rows / sec,
+            rmsnorm_gbs=round(rms["value"], 2), swiglu_gbs=round(swiglu["value"], 2),
+        )
+
+
+def _host_time(step, steps: int, warmup: int = 2) -> float:
+    """Seconds per call of ``step(None)``: ``warmup`` untimed calls, then ``steps`` calls
+    between two device synchronisations."""
+
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(None)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _other_configs(steps: int) -> dict:
+    """RoPE (q [8,2048,32,128] + k [8,2048,8,128], rotate-half, 4 layers), the fused
+    cross-entropy ([8192, 128256] bf16) and the fused AdamW step (1.2e9 fp32 parameters):
+    each built, timed by the host clock over ``steps`` steps after 2 warm-ups, and freed."""
+
+    out = {}
+    for name in ("rope", "ce", "adamw"):
+        wl = WORKLOADS[name](DEFAULT_LAYERS[name])
+        sec = _host_time(wl.step, steps)
+        gbps = wl.bytes_per_step / sec / 1e9
+        out[name] = {
+            "workload": wl.description,
+            "ms_per_step": round(sec * 1e3, 4),
+            "gbs": round(gbps, 1),
+            "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+        }
+        del wl
+        torch.cuda.empty_cache()
+    return out
 
 
 class RoPEWorkload(Workload):
@@ -887,6 +1018,242 @@ class ZeroMixedPrecisionStepWorkload(AdamWWorkload):
         )
 
 
+class ModulesWorkload(Workload):
+    """RMSNorm and SwiGLU forward + backward as picotron calls them: the ``RMSNorm`` module
+    with ``use_triton_rmsnorm=True`` (reference src/picotron/models/picotron_decoder.py:32-46)
+    and ``triton_swiglu`` inside ``SwiGLU.forward`` (src/picotron/nn/feedforward.py:26-43),
+    each through autograd (``torch.autograd.grad`` to the inputs and the weight), against the
+    same kernels called directly through the C ABI on preallocated buffers.  The value is the
+    headline shapes' algorithmic bytes over the module path's wall time; ``config.paths``
+    gives, per shape, the wall time per fwd+bwd call of both paths and the host time the
+    module path spends issuing one call (measured without synchronising, so it shows where
+    host work, not the kernels, sets the pace)."""
+
+    name = "modules"
+    metric = "RMSNorm/SwiGLU fwd+bwd through the module/autograd path, HBM GB/s & % of peak, 16k tok bf16"
+
+    SHAPES = {
+        # name: (rmsnorm shape, swiglu shape, dtype)
+        "quickstart": ((2, 64, 128), (2, 64, 256), torch.float32),
+        "headline": ((8, 2048, 4096), (8, 2048, 14336), torch.bfloat16),
+    }
+
+    def __init__(self, layers: int) -> None:
+        from picotron_amd.nn.norm import RMSNorm
+
+        self.layers = 1
+        self.cases = {}
+        for name, (rshape, sshape, dtype) in self.SHAPES.items():
+            d = rshape[-1]
+            norm = RMSNorm(d, eps=1e-5, use_triton_rmsnorm=True).to(device="cuda", dtype=dtype)
+            with torch.no_grad():
+                norm.weight.copy_(_seeded((d,), dtype, 2, 0.02, 1.0))
+            case = dict(
+                norm=norm,
+                x=_seeded(rshape, dtype, 3).requires_grad_(True),
+                dy=_seeded(rshape, dtype, 4),
+                g=_seeded(sshape, dtype, 5).requires_grad_(True),
+                u=_seeded(sshape, dtype, 6).requires_grad_(True),
+                ds=_seeded(sshape, dtype, 7),
+            )
+            s = torch.finfo(dtype).bits // 8
+            rows, cols = case["x"].numel() // d, d
+            n = case["g"].numel()
+            case["bytes"] = (2 * rows * cols * s + cols * s + 4 * rows) + (3 * rows * cols * s + 2 * cols * s + 4 * rows) \
+                + 8 * n * s
+            case["direct"] = self._direct(case, rows, cols, n, dtype)
+            self.cases[name] = case
+        self.bytes_per_step = self.cases["headline"]["bytes"]
+        self.tokens_per_step = 16384
+        self.dominant = "module path: rmsnorm fwd + bwd, swiglu fwd + bwd (5 kernels)"
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "RMSNorm(4096, use_triton_rmsnorm=True) on bf16 [8, 2048, 4096] (bf16 weight) and triton_swiglu on "
+            "bf16 [8, 2048, 14336] gate/up, forward + torch.autograd.grad to inputs and weight; step = one call "
+            "of each"
+        )
+
+    @staticmethod
+    def _direct(case, rows, cols, n, dtype):
+        """The same kernels through the C ABI on preallocated buffers (no autograd, no allocation)."""
+
+        lib = _lib.lib()
+        code = ops.dtype_code(dtype)
+        x, dy, g, u, ds = (case[k].detach() for k in ("x", "dy", "g", "u", "ds"))
+        w = case["norm"].weight.detach()
+        y, dx, gy, dg, du = (torch.empty_like(t) for t in (x, x, g, g, g))
+        rstd = torch.empty(rows, dtype=torch.float32, device="cuda")
+        dw = torch.empty_like(w)
+        ws_bytes = lib.pt_rmsnorm_bwd_workspace_bytes(rows, cols, code)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        keep = (y, dx, gy, dg, du, rstd, dw, ws)
+        calls = [
+            (lib.pt_rmsnorm_fwd, (_p(x), cols, _p(w), _p(y), cols, _p(rstd), rows, cols, ctypes.c_float(1e-5),
+                                  code, code, stream)),
+            (lib.pt_rmsnorm_bwd, (_p(dy), cols, _p(x), cols, _p(w), _p(rstd), _p(dx), cols, _p(dw), _p(ws),
+                                  ws_bytes, rows, cols, code, code, stream)),
+            (lib.pt_swiglu_fwd, (_p(g), _p(u), _p(gy), n, code, stream)),
+            (lib.pt_swiglu_bwd, (_p(ds), _p(g), _p(u), _p(dg), _p(du), n, code, stream)),
+        ]
+
+        def run():
+            for fn, args in calls:
+                rc = fn(*args)
+                if rc:
+                    _lib.check(fn.__name__, rc)
+
+        run.keep = keep
+        return run
+
+    @staticmethod
+    def _module_call(case):
+        from picotron_amd.nn.triton_kernels import triton_swiglu
+
+        norm, x, g, u = case["norm"], case["x"], case["g"], case["u"]
+        y = norm(x)
+        torch.autograd.grad(y, (x, norm.weight), case["dy"])
+        out = triton_swiglu(g, u)
+        torch.autograd.grad(out, (g, u), case["ds"])
+
+    def step(self, events):
+        case = self.cases["headline"]
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        self._module_call(case)
+        if events is not None:
+            end.record()
+
+    def extra(self, steps: int) -> dict:
+        paths = {}
+        for name, case in self.cases.items():
+            reps = steps if name == "headline" else 50 * steps
+            module = lambda: self._module_call(case)  # noqa: E731
+            for _ in range(3):
+                module()
+                case["direct"]()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                module()
+            t_issue = time.perf_counter() - t0
+            torch.cuda.synchronize()
+            t_module = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                case["direct"]()
+            torch.cuda.synchronize()
+            t_direct = time.perf_counter() - t0
+            paths[name] = {
+                "rmsnorm_shape": list(case["x"].shape),
+                "swiglu_shape": list(case["g"].shape),
+                "dtype": str(case["x"].dtype).replace("torch.", ""),
+                "calls": reps,
+                "module_wall_us_per_call": round(t_module / reps * 1e6, 2),
+                "module_host_issue_us_per_call": round(t_issue / reps * 1e6, 2),
+                "direct_c_abi_wall_us_per_call": round(t_direct / reps * 1e6, 2),
+                "module_gbs": round(case["bytes"] / (t_module / reps) / 1e9, 1),
+                "direct_gbs": round(case["bytes"] / (t_direct / reps) / 1e9, 1),
+            }
+        return {"paths": paths}
+
+    def cpu_baseline(self) -> dict:
+        return None
+
+
+class GradScalerStepWorkload(AdamWWorkload):
+    """The train loop's single-GPU fp16 update (reference src/picotron/training/train_loop.py:
+    155-160: GradScaler.unscale_, clip_grad_norm_, GradScaler.step, GradScaler.update), fused."""
+
+    name = "fp16_step"
+    metric = "Fused GradScaler unscale + inf-check + clip + AdamW step HBM GB/s & % of peak, 1.2e9 fp32 params"
+    loss_scale = 65536.0
+
+    def __init__(self, layers: int) -> None:
+        super().__init__(layers)
+        from picotron_amd.nn.triton_kernels import triton_grad_scaler_step
+
+        n = self.n
+        self.fn = triton_grad_scaler_step
+        self.g.mul_(self.loss_scale)  # gradients as the scaled loss's backward leaves them
+        self.g_scaled = self.g.clone()
+        self.prm = torch.nn.Parameter(self.p)
+        self.prm.grad = self.g
+        self.opt = torch.optim.AdamW([self.prm], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        self.scaler = torch.amp.GradScaler("cuda", init_scale=self.loss_scale)
+        self.scaler.scale(torch.ones((), device="cuda"))  # the scale tensor, as scale(loss) makes it
+        self.bytes_per_step = 36 * n  # stats: read g; step: read p, g, m, v, write p, m, v, g
+        self.dominant = ("fused GradScaler step (grad_stats_kernel + grad_stats_finish_kernel, one host read "
+                         "of the overflow flag, adamw_kernel with the combined unscale x clip multiplier, "
+                         "the scaler's update)")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "fp16 GradScaler update on one GPU: loss scale 65536, finite check, unscale, "
+            "clip_grad_norm_(1.0) (torch's rule) and the AdamW step, then the scaler's update; one flat "
+            "1.2e9-element fp32 parameter; step = triton_grad_scaler_step (each step unscales the gradients "
+            "the previous one left; the values do not change the traffic)"
+        )
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        skipped = self.fn(self.scaler, self.opt, 1.0)
+        if events is not None:
+            end.record()
+        if skipped:
+            raise RuntimeError("unexpected overflow in the synthetic gradients")
+
+    def extra(self, steps: int) -> dict:
+        """torch's own sequence on the same data and its own AdamW (foreach, the default on a
+        GPU): unscale_, clip_grad_norm_, step, update."""
+
+        prm = torch.nn.Parameter(self.p.detach().clone())
+        prm.grad = self.g_scaled.clone()
+        opt = torch.optim.AdamW([prm], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+        scaler = torch.amp.GradScaler("cuda", init_scale=self.loss_scale)
+        scaler.scale(torch.ones((), device="cuda"))
+
+        def reference(_events=None):
+            scaler.unscale_(opt)
+            torch.nn.utils.clip_grad_norm_([prm], 1.0)
+            scaler.step(opt)
+            scaler.update()
+
+        sec = _host_time(reference, steps)
+        del prm, opt
+        torch.cuda.empty_cache()
+        return {"torch_sequence_ms_per_step": round(sec * 1e3, 4)}
+
+    def cpu_baseline(self) -> dict:
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        n = 120_000_000
+        p = torch.nn.Parameter(self.p[:n].cpu())
+        g_scaled = self.g_scaled[:n].cpu()
+        p.grad = g_scaled.clone()
+        opt = torch.optim.AdamW([p], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+        scaler = torch.amp.GradScaler("cpu", init_scale=self.loss_scale)
+        scaler.scale(torch.ones(()))
+
+        def fp16_step():
+            scaler.unscale_(opt)
+            torch.nn.utils.clip_grad_norm_([p], 1.0)
+            scaler.step(opt)
+            scaler.update()
+
+        sec, calls = _time_cpu(fp16_step, setup=lambda: p.grad.copy_(g_scaled))
+        return dict(
+            value=36 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"{n:.1e} of 1.2e9 params (1/10): GradScaler.unscale_ + clip_grad_norm_(1.0) + "
+                   f"GradScaler.step (torch.optim.AdamW(foreach=False)) + update on CPU, scaled gradients "
+                   f"restored untimed before each call, median of {calls} calls (~{CPU_TARGET_S:.0f} s) "
+                   f"after 1 warm-up",
+            seconds_per_call=sec, params_per_s=n / sec,
+        )
+
+
 class CopyWorkload(Workload):
     name = "copy"
     metric = "128-bit streaming copy HBM GB/s (achievable-bandwidth reference)"
@@ -921,6 +1288,7 @@ class CopyWorkload(Workload):
 
 
 WORKLOADS = {
+    "headline": HeadlineWorkload,
     "rmsnorm": RMSNormWorkload,
     "residual_rmsnorm": ResidualRMSNormWorkload,
     "swiglu": SwiGLUWorkload,
@@ -930,11 +1298,13 @@ WORKLOADS = {
     "adamw": AdamWWorkload,
     "adamw_clip": AdamWClipWorkload,
     "zero_step": ZeroMixedPrecisionStepWorkload,
+    "fp16_step": GradScalerStepWorkload,
+    "modules": ModulesWorkload,
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
-                  "zero_step": 1, "copy": 4}
+DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
+                  "zero_step": 1, "fp16_step": 1, "modules": 1, "copy": 4}
 
 
 def _traffic(workload: str) -> dict | None:
@@ -953,7 +1323,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="rmsnorm")
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
     parser.add_argument("--layers", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra", action="store_true",
@@ -991,43 +1361,74 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
 
     # Pass 2 (the roofline): the same K steps again with a HIP event pair around every
-    # launch of the dominant kernel, recorded on the stream the kernels run on.  The event
-    # records add a few microseconds per launch, so this pass is not used for the value.
-    per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1, "ce_train": 1, "adamw": 1,
-                "adamw_clip": 1, "zero_step": 1, "copy": layers}[args.workload]
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps * per_step)]
-    pending = list(reversed(events))
+    # timed launch, recorded on the stream the kernels run on.  The event records add a few
+    # microseconds per launch, so this pass is not used for the value.  A workload with
+    # several launch kinds (timed_kinds) gets one event list per kind; the others time their
+    # dominant launch.
+    kinds = getattr(wl, "timed_kinds", None)
+    if kinds is None:
+        per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1,
+                    "ce_train": 1, "adamw": 1, "adamw_clip": 1, "zero_step": 1, "fp16_step": 1,
+                    "modules": 1, "copy": layers}[args.workload]
+        kinds = {"dominant": per_step}
+    events = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.steps * n)] for k, n in kinds.items()}
+    pending = {k: list(reversed(v)) for k, v in events.items()}
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     for _ in range(args.steps):
-        wl.step(pending)
+        wl.step(pending if hasattr(wl, "timed_kinds") else pending["dominant"])
     torch.cuda.synchronize()
     elapsed_instrumented = time.perf_counter() - t1
 
     ms_per_step = elapsed / args.steps * 1e3
     gbps = wl.bytes_per_step / (elapsed / args.steps) / 1e9
-    launch_ms = [s.elapsed_time(e) for s, e in events]
-    avg_us = statistics.mean(launch_ms) * 1e3
-    achieved = wl.dominant_bytes / (avg_us * 1e-6) / 1e9
     traffic = _traffic(args.workload)
+    per_kernel = {}
+    for kind, pairs in events.items():
+        launch_ms = [a.elapsed_time(b) for a, b in pairs]
+        info = wl.kinds[kind] if kind in getattr(wl, "kinds", {}) else {"kernel": wl.dominant,
+                                                                         "bytes": wl.dominant_bytes}
+        avg_us = statistics.mean(launch_ms) * 1e3
+        achieved = info["bytes"] / (avg_us * 1e-6) / 1e9
+        entry = {
+            "kernel": info["kernel"],
+            "algorithmic_bytes_per_launch": info["bytes"],
+            "avg_launch_us": round(avg_us, 2),
+            "median_launch_us": round(statistics.median(launch_ms) * 1e3, 2),
+            "launches_timed": len(launch_ms),
+            "achieved": round(achieved, 1),
+            "frac": round(achieved / PEAK_GBPS, 4),
+            "traffic": None,
+            "total_ms": sum(launch_ms),
+        }
+        if traffic:
+            per = traffic.get("kernels", {}).get(kind) if "kernels" in traffic and isinstance(traffic["kernels"], dict) else traffic
+            if per:
+                entry["traffic"] = per.get("bytes_per_launch")
+        per_kernel[kind] = entry
+    dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_ms"])
+    dom = per_kernel[dominant]
     roofline = {
         "bound": "hbm",
-        "achieved": round(achieved, 1),
+        "achieved": dom["achieved"],
         "peak": PEAK_GBPS,
         "unit": "GB/s",
-        "frac": round(achieved / PEAK_GBPS, 4),
-        "traffic": traffic.get("bytes_per_launch") if traffic else None,
-        "kernel": wl.dominant,
-        "algorithmic_bytes_per_launch": wl.dominant_bytes,
-        "avg_launch_us": round(avg_us, 2),
-        "median_launch_us": round(statistics.median(launch_ms) * 1e3, 2),
-        "launches_timed": len(launch_ms),
+        "frac": dom["frac"],
+        "traffic": dom["traffic"],
+        "kernel": dom["kernel"],
+        "algorithmic_bytes_per_launch": dom["algorithmic_bytes_per_launch"],
+        "avg_launch_us": dom["avg_launch_us"],
+        "median_launch_us": dom["median_launch_us"],
+        "launches_timed": dom["launches_timed"],
         "timing": "HIP events around each launch, in a second pass of the same steps",
         "ms_per_step_with_events": round(elapsed_instrumented / args.steps * 1e3, 4),
     }
     if traffic:
         roofline["traffic_source"] = traffic.get("source")
+    if len(per_kernel) > 1:
+        roofline["per_kernel"] = {k: {kk: vv for kk, vv in v.items() if kk != "total_ms"}
+                                  for k, v in per_kernel.items()}
 
     extra = None if args.no_extra else wl.extra(args.steps)
 
