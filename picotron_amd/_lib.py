@@ -205,5 +205,16 @@ def check(fn: str, rc: int) -> None:
         raise HipKernelError(fn, rc, message.decode() if message else "")
 
 
+_bound: dict[str, object] = {}
+
+
 def call(fn: str, *args) -> None:
-    check(fn, getattr(lib(), fn)(*args))
+    """Call entry point ``fn`` and raise :class:`HipKernelError` on a nonzero return (the bound
+    function object is looked up once per name)."""
+
+    f = _bound.get(fn)
+    if f is None:
+        f = _bound[fn] = getattr(lib(), fn)
+    rc = f(*args)
+    if rc != PT_OK:
+        check(fn, rc)

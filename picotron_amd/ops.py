@@ -33,8 +33,22 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The device's current HIP stream as an integer handle (torch's raw-stream query when
+    present: it skips building a Stream object on every launch)."""
+
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+@functools.lru_cache(maxsize=256)
+def _rmsnorm_ws_bytes(rows: int, cols: int, code: int) -> int:
+    return int(_lib.lib().pt_rmsnorm_bwd_workspace_bytes(rows, cols, code))
 
 
 def _ptr(t: Tensor | None) -> int | None:
@@ -120,7 +134,7 @@ def rmsnorm_bwd(
     ws = None
     ws_bytes = 0
     if need_dw:
-        ws_bytes = _lib.lib().pt_rmsnorm_bwd_workspace_bytes(rows, cols, dtype_code(x.dtype))
+        ws_bytes = _rmsnorm_ws_bytes(rows, cols, dtype_code(x.dtype))
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
     if not need_dx and not need_dw:
         return None, None
@@ -200,7 +214,7 @@ def residual_rmsnorm_bwd(
     dw = torch.empty(cols, dtype=weight.dtype, device=device) if need_dw else None
     ws, ws_bytes = None, 0
     if need_dw:
-        ws_bytes = _lib.lib().pt_rmsnorm_bwd_workspace_bytes(rows, cols, dtype_code(h.dtype))
+        ws_bytes = _rmsnorm_ws_bytes(rows, cols, dtype_code(h.dtype))
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=device)
     _lib.call(
         "pt_residual_rmsnorm_bwd",
