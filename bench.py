@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_clip|zero_step|fp16_step|modules|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
 
 Default workload (the headline metric, "RMSNorm/SwiGLU fwd+bwd"): ``--layers`` decoder layers
 (default 4), each with its own activations: the RMSNorm forward of a bf16 [16384 tokens
@@ -525,11 +525,12 @@ def _host_time(step, steps: int, warmup: int = 2) -> float:
 
 def _other_configs(steps: int) -> dict:
     """RoPE (q [8,2048,32,128] + k [8,2048,8,128], rotate-half, 4 layers), the fused
-    cross-entropy ([8192, 128256] bf16) and the fused AdamW step (1.2e9 fp32 parameters):
+    cross-entropy ([8192, 128256] bf16) and the fused AdamW step (1.2e9 fp32 parameters, as one
+    tensor and as 100):
     each built, timed by the host clock over ``steps`` steps after 2 warm-ups, and freed."""
 
     out = {}
-    for name in ("rope", "ce", "adamw"):
+    for name in ("rope", "ce", "adamw", "adamw_list"):
         wl = WORKLOADS[name](DEFAULT_LAYERS[name])
         sec = _host_time(wl.step, steps)
         gbps = wl.bytes_per_step / sec / 1e9
@@ -818,6 +819,83 @@ class AdamWWorkload(Workload):
             sample=f"{n:.1e} of 1.2e9 params (1/10): torch.optim.AdamW(foreach=False).step() (the reference "
                    f"fallback, adamw.py:47) on CPU, median of {calls} calls (~{CPU_TARGET_S:.0f} s) after "
                    f"1 warm-up",
+            seconds_per_call=sec, params_per_s=n / sec,
+        )
+
+
+class AdamWListWorkload(Workload):
+    """The fused AdamW step over a list of 100 fp32 parameters (1.2e9 elements in all), as a
+    model's parameter list reaches torch.optim.AdamW (reference src/picotron/training/
+    train_loop.py:308-325): the sizes of a decoder stack's projections (16.8M, 4.2M, 58.7M-class
+    matrices) with ten 4096-element norm weights among them, each tensor its own allocation, one
+    launch for all of them."""
+
+    name = "adamw_list"
+    metric = "Fused AdamW step HBM GB/s & % of peak, 100 fp32 tensors, 1.2e9 params"
+    dtype = "f32"
+
+    # per group: four attention projections (16.8M, 4.2M, 4.2M, 16.8M elements), three MLP
+    # projections (25.2M), two 1M-element tensors and one 4096-element norm weight
+    GROUP = [16_777_216, 4_194_304, 4_194_304, 16_777_216, 25_165_824, 25_165_824, 25_165_824,
+             1_048_576, 1_048_576, 4096]
+
+    def __init__(self, layers: int) -> None:
+        self.layers = 1
+        sizes = self.GROUP * 10
+        # pad the last matrix so the total is exactly 1.2e9 elements (a multiple of 1024 keeps
+        # every tensor a whole number of 16-byte vectors)
+        sizes[-2] += 1_200_000_000 - sum(sizes)
+        assert sum(sizes) == 1_200_000_000 and len(sizes) == 100
+        self.sizes = sizes
+        self.n = sum(sizes)
+        self.p = [_seeded((k,), torch.float32, 200 + i, 0.02) for i, k in enumerate(sizes)]
+        self.g = [_seeded((k,), torch.float32, 400 + i, 1e-3) for i, k in enumerate(sizes)]
+        self.m = [torch.zeros(k, dtype=torch.float32, device="cuda") for k in sizes]
+        self.v = [torch.zeros(k, dtype=torch.float32, device="cuda") for k in sizes]
+        host, blocks = ops.adamw_table(self.p, self.g, self.m, self.v)
+        self.table = host.cuda()
+        self.blocks = blocks
+        self.t = 1
+        self.bytes_per_step = 28 * self.n
+        self.tokens_per_step = self.n
+        self.dominant = "adamw_kernel (100 tensors, one launch)"
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            "fused AdamW over 100 fp32 parameters of decoder-projection sizes (1.2e9 elements, ten "
+            "4096-element norm weights among them), each its own allocation, lr 3e-4, betas (0.9, 0.95), "
+            "eps 1e-8, wd 0.1; step = one optimizer step (one launch)"
+        )
+        self.lib = _lib.lib()
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def step(self, events):
+        if events is not None:
+            start, end = events.pop()
+            start.record()
+        rc = self.lib.pt_adamw_step(_p(self.table), len(self.sizes), self.blocks, 3e-4, 0.9, 0.95, 1e-8, 0.1,
+                                    float(self.t), self.stream)
+        if events is not None:
+            end.record()
+        self.t += 1
+        if rc:
+            _lib.check("pt_adamw_step", rc)
+
+    def cpu_baseline(self) -> dict:
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        params = []
+        for p, g in zip(self.p[:10], self.g[:10]):
+            q = torch.nn.Parameter(p.cpu())
+            q.grad = g.cpu()
+            params.append(q)
+        n = sum(q.numel() for q in params)
+        opt = torch.optim.AdamW(params, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, foreach=False)
+        sec, calls = _time_cpu(opt.step)
+        return dict(
+            value=28 * n / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"the first 10 of the 100 tensors ({n:.2e} params, one group of sizes): "
+                   f"torch.optim.AdamW(foreach=False).step() on CPU, median of {calls} calls "
+                   f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, params_per_s=n / sec,
         )
 
@@ -1296,6 +1374,7 @@ WORKLOADS = {
     "ce": CrossEntropyWorkload,
     "ce_train": CrossEntropyTrainWorkload,
     "adamw": AdamWWorkload,
+    "adamw_list": AdamWListWorkload,
     "adamw_clip": AdamWClipWorkload,
     "zero_step": ZeroMixedPrecisionStepWorkload,
     "fp16_step": GradScalerStepWorkload,
@@ -1303,7 +1382,7 @@ WORKLOADS = {
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_clip": 1,
+DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
                   "zero_step": 1, "fp16_step": 1, "modules": 1, "copy": 4}
 
 
@@ -1368,7 +1447,7 @@ def main() -> int:
     kinds = getattr(wl, "timed_kinds", None)
     if kinds is None:
         per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1,
-                    "ce_train": 1, "adamw": 1, "adamw_clip": 1, "zero_step": 1, "fp16_step": 1,
+                    "ce_train": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1, "zero_step": 1, "fp16_step": 1,
                     "modules": 1, "copy": layers}[args.workload]
         kinds = {"dominant": per_step}
     events = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))

@@ -123,24 +123,54 @@ def test_fp32_training_step_matches_the_fallback_model(gpu):
                                    atol=1e-5 * float(st_r["exp_avg"].abs().max()))
 
 
+def _fp32_grads(model, ids):
+    """The fallback model's gradients without autocast: the precision the reduced-precision
+    runs are measured against."""
+
+    model.zero_grad(set_to_none=True)
+    logits = model(ids)
+    F.cross_entropy(logits[:, :-1, :].transpose(1, 2), ids[:, 1:]).backward()
+    grads = {n: p.grad.detach().double().clone() for n, p in model.named_parameters()}
+    model.zero_grad(set_to_none=True)
+    return grads
+
+
+# The fused path's gradient error against the fp32 model may exceed the reference's own
+# reduced-precision error by at most this factor, per parameter (measured on MI355X:
+# 0.90-1.10 for bf16 and fp16 autocast).
+ERROR_RATIO = 1.25
+
+
+def _check_error_budget(grads_f, grads_r, grads_32):
+    for name, g32 in grads_32.items():
+        norm = float(g32.norm())
+        err_r = float((grads_r[name].double() - g32).norm()) / norm
+        err_f = float((grads_f[name].double() - g32).norm()) / norm
+        assert err_f <= ERROR_RATIO * err_r + 1e-6, (name, err_f, err_r)
+        cos = F.cosine_similarity(grads_f[name].flatten().double(), grads_r[name].flatten().double(), dim=0)
+        assert float(cos) > 0.999, (name, float(cos))
+
+
 def test_bf16_autocast_training_step_tracks_the_fallback_model(gpu):
     # Under autocast the kernels see the training dtypes: fp32 residual stream into the
     # norms, bf16 gate/up into SwiGLU, bf16 query/key into RoPE, bf16 logits into the loss.
+    # Parity bar: per parameter, the fused run's gradient is no further from the fp32 model's
+    # than the reference's own bf16 run is (within ERROR_RATIO).
     reference, fused = _models(gpu)
     ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(4)).to(gpu)
+    grads_32 = _fp32_grads(reference, ids)
     with _no_fallback_warning():
         loss_f, grads_f, _ = _step(fused, True, ids, eps=1e-8, autocast=True)
     loss_r, grads_r, _ = _step(reference, False, ids, eps=1e-8, autocast=True)
     assert abs(loss_f.item() - loss_r.item()) <= 5e-3 * abs(loss_r.item())
-    for name, g in grads_r.items():
-        cos = F.cosine_similarity(grads_f[name].flatten().double(), g.flatten().double(), dim=0)
-        assert float(cos) > 0.999, (name, float(cos))
+    _check_error_budget(grads_f, grads_r, grads_32)
 
 
 def test_fp16_autocast_with_loss_scaling_tracks_the_fallback_model(gpu):
     # The fp16 path of the train loop (train_loop.py:154-159: grad_scaler.scale(loss).backward()):
     # fp16 gate/up, query/key and logits, and a loss gradient equal to the scale, which the
-    # fused cross-entropy applies on the device; gradients compared after unscaling.
+    # fused cross-entropy applies on the device; gradients compared after unscaling, with the
+    # same error-budget bar as the bf16 test.
     reference, fused = _models(gpu)
     ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(5)).to(gpu)
     scale = 4096.0
@@ -153,14 +183,14 @@ def test_fp16_autocast_with_loss_scaling_tracks_the_fallback_model(gpu):
         (loss * scale).backward()
         return loss.detach().float(), {n: p.grad.detach() / scale for n, p in model.named_parameters()}
 
+    grads_32 = _fp32_grads(reference, ids)
     with _no_fallback_warning():
         loss_f, grads_f = scaled_step(fused, True)
     loss_r, grads_r = scaled_step(reference, False)
     assert abs(loss_f.item() - loss_r.item()) <= 5e-3 * abs(loss_r.item())
-    for name, g in grads_r.items():
-        assert bool(torch.isfinite(grads_f[name]).all()), name
-        cos = F.cosine_similarity(grads_f[name].flatten().double(), g.flatten().double(), dim=0)
-        assert float(cos) > 0.999, (name, float(cos))
+    for name, g in grads_f.items():
+        assert bool(torch.isfinite(g).all()), name
+    _check_error_budget(grads_f, grads_r, grads_32)
 
 
 @contextlib.contextmanager
