@@ -202,3 +202,54 @@ def _no_fallback_warning():
         yield
     fallbacks = [str(w.message) for w in records if "PyTorch fallback" in str(w.message)]
     assert not fallbacks, fallbacks
+
+
+def test_fp16_grad_scaler_training_steps_track_the_fallback_loop(gpu):
+    """Three steps of the train loop's fp16 branch (train_loop.py:155-160, GradScaler created
+    at :292-296): fp16 autocast, the scaled loss's backward, then unscale_, clip, step and
+    update -- fused (the fused loss and AdamWStepWithFallback.step_with_grad_scaler) against the
+    reference modules with F.cross_entropy and torch's own four calls.  The scaler's state must
+    agree exactly, the losses track each other, and the parameters stay finite and close."""
+
+    reference, fused = _models(gpu)
+    ids = torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(6)).to(gpu)
+    hp = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    runs = []
+    for model, use_fused in ((fused, True), (reference, False)):
+        runs.append(dict(
+            model=model, fused=use_fused,
+            opt=torch.optim.AdamW(model.parameters(), foreach=False, **hp),
+            scaler=torch.amp.GradScaler("cuda", init_scale=2.0 ** 12, growth_interval=2),
+            loss_fn=CrossEntropyWithFallback(use_triton=use_fused, inplace=True),
+            stepper=AdamWStepWithFallback(use_triton=use_fused),
+        ))
+    for step in range(3):
+        losses = []
+        for run in runs:
+            run["opt"].zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.float16):
+                logits = run["model"](ids)
+                loss = run["loss_fn"](logits, ids, shift=True)
+            run["scaler"].scale(loss).backward()
+            if run["fused"]:
+                with _no_fallback_warning():
+                    run["stepper"].step_with_grad_scaler(run["scaler"], run["opt"], 1.0)
+            else:
+                run["scaler"].unscale_(run["opt"])
+                torch.nn.utils.clip_grad_norm_(run["model"].parameters(), 1.0)
+                run["scaler"].step(run["opt"])
+                run["scaler"].update()
+            losses.append(loss.item())
+        f, r = runs
+        assert f["scaler"].get_scale() == r["scaler"].get_scale(), step
+        assert f["scaler"]._growth_tracker.item() == r["scaler"]._growth_tracker.item(), step
+        assert abs(losses[0] - losses[1]) <= 5e-3 * abs(losses[1]), (step, losses)
+    for (name, p_f), p_r in zip(fused.named_parameters(), reference.parameters()):
+        assert bool(torch.isfinite(p_f).all()), name
+        # three Adam updates of at most lr each: the runs may differ only where a gradient's
+        # sign is within its fp16 rounding, so by far most elements agree closely
+        diff = (p_f.detach() - p_r.detach()).abs()
+        assert float(diff.max()) <= 6.01 * hp["lr"], name
+        assert float((diff > 0.1 * hp["lr"]).float().mean()) < 0.02, name
+    # growth_interval 2 over three clean steps: the scale doubled once
+    assert runs[0]["scaler"].get_scale() == 2.0 ** 13
