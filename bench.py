@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|ce_train_fp16|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
 
 Default workload (the headline metric, "RMSNorm/SwiGLU fwd+bwd"): ``--layers`` decoder layers
 (default 4), each with its own activations: the RMSNorm forward of a bf16 [16384 tokens
@@ -107,6 +107,7 @@ class Workload:
     dominant_bytes = 0
     bytes_per_step = 0
     tokens_per_step = 0
+    launches_per_step = 1  # timed launches of the dominant kernel per step (one per layer where layered)
 
     def step(self, events: list | None) -> None:
         raise NotImplementedError
@@ -127,6 +128,7 @@ class RMSNormWorkload(Workload):
 
     def __init__(self, layers: int) -> None:
         self.layers = layers
+        self.launches_per_step = layers
         r, c = self.rows, self.cols
         self.w = _seeded((c,), torch.bfloat16, 2, 0.02, 1.0)
         self.x = [_seeded((r, c), torch.bfloat16, 10 + i) for i in range(layers)]
@@ -245,6 +247,7 @@ class ResidualRMSNormWorkload(Workload):
 
     def __init__(self, layers: int) -> None:
         self.layers = layers
+        self.launches_per_step = layers
         r, c = self.rows, self.cols
         bf = torch.bfloat16
         self.w = _seeded((c,), bf, 2, 0.02, 1.0)
@@ -361,6 +364,7 @@ class SwiGLUWorkload(Workload):
 
     def __init__(self, layers: int) -> None:
         self.layers = layers
+        self.launches_per_step = layers
         n = self.rows * self.cols
         self.n = n
         self.g = [_seeded((n,), torch.bfloat16, 30 + i) for i in range(layers)]
@@ -553,6 +557,7 @@ class RoPEWorkload(Workload):
         from picotron_amd.nn.rope import rotary_cos_sin
 
         self.layers = layers
+        self.launches_per_step = layers
         self.layout = layout
         b, s, hq, hk, d = 8, 2048, 32, 8, 128
         self.cos, self.sin = rotary_cos_sin(s, d, 500_000.0, device=torch.device("cuda"), dtype=torch.float32)
@@ -734,7 +739,8 @@ class CrossEntropyTrainWorkload(Workload):
 
     def extra(self, steps: int) -> dict:
         """The same loss through the reference's call shape (sliced, transposed view), whose
-        backward adds autograd's slice backward: a zero-filled full-size gradient plus a copy."""
+        backward adds autograd's slice backward: a zero-filled full-size gradient plus a copy;
+        and the reference's own call, F.cross_entropy under bf16 autocast, on the same logits."""
 
         for _ in range(2):
             self._step(False)
@@ -744,7 +750,19 @@ class CrossEntropyTrainWorkload(Workload):
             self._step(False)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) / steps * 1e3
-        return {"sliced_view_call_ms_per_step": round(ms, 4)}
+        leaf = self.leaf.detach().clone().requires_grad_(True)
+
+        def reference(_events=None):
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = torch.nn.functional.cross_entropy(
+                    leaf.view(self.b, self.s, self.vocab)[:, :-1, :].transpose(1, 2), self.ids[:, 1:])
+            torch.autograd.grad(loss, leaf)
+
+        ref_ms = _host_time(reference, min(steps, 5), warmup=1) * 1e3
+        del leaf
+        torch.cuda.empty_cache()
+        return {"sliced_view_call_ms_per_step": round(ms, 4),
+                "torch_autocast_bf16_ms_per_step": round(ref_ms, 4)}
 
     def cpu_baseline(self) -> dict:
         from oracle import cross_entropy as o_ce
@@ -764,6 +782,64 @@ class CrossEntropyTrainWorkload(Workload):
                    f"calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=self.b * (s - 1) / sec,
         )
+
+
+class CrossEntropyTrainFp16Workload(CrossEntropyTrainWorkload):
+    """The train loop's loss under fp16 autocast with a GradScaler (reference
+    src/picotron/training/train_loop.py:141-144,155-160): fp16 logits, the loss scaled by 65536
+    before its backward.  The fp16 forward reads the logits and keeps each row's log-sum-exp; the
+    backward reads them again and writes the gradient with the scale applied, rounded once."""
+
+    name = "ce_train_fp16"
+    metric = ("Next-token cross-entropy fwd + autograd bwd (fp16, loss scale 65536) HBM GB/s & % of peak, "
+              "logits [4, 2049, 128256]")
+    dtype = "f16"
+    loss_scale = 65536.0
+
+    def __init__(self, layers: int) -> None:
+        super().__init__(layers)
+        b, s, v = self.b, self.s, self.vocab
+        self.leaf = self.leaf.detach().half().requires_grad_(True)
+        rows = b * s
+        self.bytes_per_step = 3 * rows * v * 2 + 16 * rows  # forward: read; backward: read + write
+        self.dominant = ("shifted cross-entropy fp16 forward + autograd backward (ce_prepare_kernel + "
+                         "ce_rows_kernel + ce_finish_kernel, then ce_scale_kernel writing the gradient)")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            f"train-loop loss on fp16 model logits [{b}, {s}, {v}] ~N(0,2^2) against input_ids[:, 1:] "
+            f"(5% = -100), loss x 65536 (a GradScaler's scale) before torch.autograd.grad to the logits' "
+            f"leaf; the forward reads the logits once, the backward reads them and writes the gradient"
+        )
+
+    def _step(self, shifted: bool):
+        logits = self.leaf.view(self.b, self.s, self.vocab)
+        if shifted:
+            loss = self.fn(logits, self.ids, shift=True)
+        else:
+            loss = self.fn(logits[:, :-1, :].transpose(1, 2), self.ids[:, 1:])
+        (grad,) = torch.autograd.grad(loss * self.loss_scale, self.leaf)
+        return grad
+
+    def extra(self, steps: int) -> dict:
+        """The reference's call under fp16 autocast (F.cross_entropy upcasts to fp32) on the same
+        logits, its backward with the same scale."""
+
+        leaf = self.leaf.detach().clone().requires_grad_(True)
+        ids = self.ids
+
+        def reference(_events=None):
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = torch.nn.functional.cross_entropy(
+                    leaf.view(self.b, self.s, self.vocab)[:, :-1, :].transpose(1, 2), ids[:, 1:])
+            torch.autograd.grad(loss * self.loss_scale, leaf)
+
+        sec = _host_time(reference, min(steps, 5), warmup=1)
+        del leaf
+        torch.cuda.empty_cache()
+        return {"torch_autocast_fp16_ms_per_step": round(sec * 1e3, 4)}
+
+    def cpu_baseline(self) -> dict:
+        return None
 
 
 class AdamWWorkload(Workload):
@@ -1340,6 +1416,7 @@ class CopyWorkload(Workload):
 
     def __init__(self, layers: int) -> None:
         self.layers = layers
+        self.launches_per_step = layers
         self.src = [torch.empty(self.nbytes, dtype=torch.uint8, device="cuda").fill_(i) for i in range(layers)]
         self.dst = [torch.empty(self.nbytes, dtype=torch.uint8, device="cuda") for _ in range(layers)]
         self.bytes_per_step = layers * 2 * self.nbytes
@@ -1373,6 +1450,7 @@ WORKLOADS = {
     "rope": RoPEWorkload,
     "ce": CrossEntropyWorkload,
     "ce_train": CrossEntropyTrainWorkload,
+    "ce_train_fp16": CrossEntropyTrainFp16Workload,
     "adamw": AdamWWorkload,
     "adamw_list": AdamWListWorkload,
     "adamw_clip": AdamWClipWorkload,
@@ -1382,7 +1460,7 @@ WORKLOADS = {
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
+DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "ce_train_fp16": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
                   "zero_step": 1, "fp16_step": 1, "modules": 1, "copy": 4}
 
 
@@ -1446,10 +1524,7 @@ def main() -> int:
     # dominant launch.
     kinds = getattr(wl, "timed_kinds", None)
     if kinds is None:
-        per_step = {"rmsnorm": layers, "residual_rmsnorm": layers, "swiglu": layers, "rope": layers, "ce": 1,
-                    "ce_train": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1, "zero_step": 1, "fp16_step": 1,
-                    "modules": 1, "copy": layers}[args.workload]
-        kinds = {"dominant": per_step}
+        kinds = {"dominant": wl.launches_per_step}
     events = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                   for _ in range(args.steps * n)] for k, n in kinds.items()}
     pending = {k: list(reversed(v)) for k, v in events.items()}

@@ -159,11 +159,11 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
  * loss_out (fp32 scalar, device) = sum(lse - logit[target]) / n_valid.
  * If write_grad != 0 the logits are overwritten IN PLACE with
  *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows)
- * for fp32 and bf16.  fp16 logits receive (softmax - onehot(target)) * 2^15 * q / n_valid
- * instead, q the largest power of two not above n_valid: the loss scale of fp16 training
- * arrives only with the backward, and softmax / n_valid is mostly below fp16's smallest
- * subnormal at language-model sizes.  The fp16 gradient is complete once
- * pt_cross_entropy_scale_grad has run (always needed for fp16).
+ * for fp32 and bf16.  fp16 logits are left unchanged and each row's log-sum-exp is kept in
+ * the workspace: the loss scale of fp16 training arrives only with the backward, and
+ * softmax / n_valid is mostly below fp16's smallest subnormal at language-model sizes, so
+ * pt_cross_entropy_scale_grad (always needed for fp16) writes the gradient, scale included,
+ * rounding to fp16 once.
  * A non-ignored target outside [0, vocab) makes that row's loss NaN and sets
  * *(int32*)status bit 0; status is part of the workspace (see below).
  * Replaces CrossEntropyWithFallback / triton_cross_entropy
@@ -182,11 +182,11 @@ int32_t* pt_cross_entropy_status(void* workspace);
 /* Multiply a gradient written by pt_cross_entropy (same row and target description) by
  * the fp32 scalar at *grad_output (device memory), skipping all work when it equals 1.0
  * exactly; rows whose target is ignore_index stay zero.  This is the backward of the fused
- * loss: the logits already hold d(mean loss)/d(logits).  For fp16 the rows hold
- * (softmax - onehot) * 2^15 * q / n_valid and are multiplied by *grad_output * 2^-15 / q in
- * fp32, then rounded to fp16 (always, also for a grad_output of 1; an exact rescaling when
- * grad_output is a power of two); n_valid is read from `workspace`, the forward call's
- * workspace, which must then be non-NULL (fp32 and bf16 ignore it). */
+ * loss: the logits already hold d(mean loss)/d(logits).  For fp16 the logits are still the
+ * logits and each element becomes (exp(x - lse) - onehot) * (*grad_output / n_valid), computed
+ * in fp32 and rounded to fp16 once (always, also for a grad_output of 1); lse and n_valid are
+ * read from `workspace`, the forward call's workspace, which must then be non-NULL (fp32 and
+ * bf16 ignore it). */
 int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
                                 int64_t outer_stride, int64_t inner_stride, int64_t vocab,
                                 const int64_t* targets, int64_t t_outer_stride,

@@ -18,7 +18,9 @@
 //      element's gradient (softmax_t - 1) / n_valid comes from the exact fp32 target logit.
 //      Longer or unaligned rows use ce_rows_batched (two passes, batches of loads in flight,
 //      the second pass served largely by the Infinity Cache).
-//      Each row's fp32 loss goes to the workspace.
+//      Each row's fp32 loss goes to the workspace.  fp16 logits are left as they are: the
+//      row's log-sum-exp goes to the workspace instead, and the backward (ce_scale) writes the
+//      gradient with grad_output applied, rounding to fp16 once.
 //   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
 //      n_valid, so the loss is bitwise reproducible.
 // exp(x - m) is evaluated as exp2((x - m) * log2(e)) on the hardware exp2 unit.
@@ -39,7 +41,7 @@ struct CeWork {
   int reserved;
   int status;     // bit 0: a non-ignored target outside [0, vocab)
   int pad;
-  // followed by float row_loss[rows], 16-byte aligned
+  // followed by float row_loss[rows] (16-byte aligned), then float row_lse[rows]
 };
 
 constexpr size_t kHeader = 16;
@@ -47,6 +49,24 @@ constexpr size_t kHeader = 16;
 __device__ __forceinline__ float* row_losses(CeWork* ws) {
   return reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + kHeader);
 }
+
+// Log-sum-exp of each row, kept for a deferred gradient (fp16); `rows` is the call's row count.
+__device__ __forceinline__ const float* row_lses(const CeWork* ws, int64_t rows) {
+  return reinterpret_cast<const float*>(reinterpret_cast<const char*>(ws) + kHeader) + rows;
+}
+__device__ __forceinline__ float* row_lses(CeWork* ws, int64_t rows) {
+  return row_losses(ws) + rows;
+}
+
+// What the row kernels do with the gradient.  kGradWrite: write d(mean loss)/d(logits) over
+// the logits.  kGradDefer (fp16): leave the logits as they are and keep each row's
+// log-sum-exp; the backward then writes the gradient, grad_output included, rounding to fp16
+// once.  fp16 cannot hold softmax / n_valid (about 1e-10 for vocab 128256 over 8192 rows: below
+// its smallest subnormal) until the loss scale of fp16 training, which only arrives with the
+// backward, lifts it.
+constexpr int kGradNone = 0;
+constexpr int kGradWrite = 1;
+constexpr int kGradDefer = 2;
 
 __device__ __forceinline__ float inv_n_of(const CeWork* ws) { return 1.0f / ws->n_valid; }
 
@@ -119,7 +139,7 @@ __device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t v
   T* p = logits + o * os + ii * is;
   const int64_t tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
   if (tgt == ignore_index) {
-    if (write_grad) {
+    if (write_grad == kGradWrite) {
       for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
         if constexpr (ALIGNED) {
           store16<true>(p + e, u32x4{0u, 0u, 0u, 0u});
@@ -193,32 +213,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(void* base, int byt
 template <typename T>
 constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
 
-// Scale of the gradient the row kernels write.  fp32 and bf16 rows receive d(mean loss) /
-// d(logits) = (softmax - onehot) / n_valid itself.  fp16 rows receive
-// (softmax - onehot) * 2^15 * q / n_valid, q the largest power of two not above n_valid (a
-// factor in (2^14, 2^15]): a GradScaler's loss scale only arrives with the backward, and
-// softmax / n_valid (about 1e-10 for vocab 128256 over 8192 rows) lies below fp16's smallest
-// subnormal, so stored unscaled nearly every gradient would be 0 before that scale could
-// lift it.  The factor keeps probabilities down to 2^-28 normal (|softmax - onehot| <= 1
-// keeps the values at most 32768 < 65504).  The backward always runs for fp16 and multiplies
-// by grad_output * 2^-15 / q: for a power-of-two grad_output (a GradScaler's scale, or 1) an
-// exact rescaling, so the gradient is rounded no more often than on the other types.
-constexpr float kF16GradScale = 32768.0f;
-
-// The largest power of two not above n (n >= 1): n with its mantissa bits cleared.
-__device__ __forceinline__ float pow2_floor(float n) {
-  return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, n) & 0xff800000u);
-}
-
-template <typename T>
-__device__ __forceinline__ float grad_factor(const CeWork* ws) {
-  if constexpr (std::is_same<T, _Float16>::value) {
-    return (kF16GradScale * pow2_floor(ws->n_valid)) / ws->n_valid;
-  } else {
-    return inv_n_of(ws);
-  }
-}
-
 // The bit pattern of two / one -inf in the storage type, for masking vectors past the row.
 template <typename T>
 constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000u
@@ -259,7 +253,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   const auto buf = row_buffer(logits + cur.off, row_bytes);
 
   if (cur.skip) {
-    if (write_grad) {
+    if (write_grad == kGradWrite) {
 #pragma unroll
       for (int k = 0; k < VPT; ++k)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf,
@@ -341,13 +335,14 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) S += red_s[w] * exp_shifted(red_m[w], refM);
   if (tid == owner) row_losses(ws)[row] = row_loss(M, S, xt);
-  if (!write_grad) return;
+  if (write_grad == kGradDefer && tid == 0) row_lses(ws, gridDim.x)[row] = M + __logf(S);
+  if (write_grad != kGradWrite) return;
 
-  const float scale = grad_factor<T>(ws) / S;
+  const float scale = inv_n_of(ws) / S;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     Vec16<T> out;
-    // exp(m_k - M) / (S n) per chunk (2^15 / S for fp16); 0 for a chunk whose reference is -inf (it held only
+    // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf (it held only
     // -inf logits, whose exps are 0).
     const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
 #pragma unroll
@@ -361,7 +356,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
   if (!bad && tid == owner) {
     Vec16<T> one;
-    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, grad_factor<T>(ws)));
+    one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n_of(ws)));
     const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
     if constexpr (sizeof(T) == 4) {
       __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
@@ -417,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   const int my_edge = tid < head ? tid : (kThreads - 1 - tid < ntail ? tail_start + (kThreads - 1 - tid) : -1);
 
   if (cur.skip) {
-    if (write_grad) {
+    if (write_grad == kGradWrite) {
       for (int b = 0; b < body_bytes; b += kChunkBytes)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf, voff + b, 0,
                                                kNonTemporal);
@@ -511,9 +506,10 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   for (int w = 0; w < kWaves; ++w) S += red_s[w] * exp_shifted(red_m[w], refM);
   const float xt = s_xt;
   if (tid == 0) row_losses(ws)[row] = row_loss(M, S, xt);
-  if (!write_grad) return;
+  if (write_grad == kGradDefer && tid == 0) row_lses(ws, gridDim.x)[row] = M + __logf(S);
+  if (write_grad != kGradWrite) return;
 
-  const float inv_n = grad_factor<T>(ws);
+  const float inv_n = inv_n_of(ws);
   const float scale = inv_n / S;
 #pragma unroll
   for (int k = 0; k < KEEP; ++k) {
@@ -618,9 +614,11 @@ __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
   const float se = block_reduce_sum(mine, red);
   const float xt = s_target_logit;
   if (threadIdx.x == 0) row_losses(ws)[blockIdx.x] = row_loss(mx, se, xt);
-  if (!write_grad) return;
+  if (write_grad == kGradDefer && threadIdx.x == 0)
+    row_lses(ws, gridDim.x)[blockIdx.x] = mx + __logf(se);
+  if (write_grad != kGradWrite) return;
 
-  const float inv_n = grad_factor<T>(ws);
+  const float inv_n = inv_n_of(ws);
   const float scale = inv_n / se;
   const float gt = target_grad(mx, se, xt, inv_n);
   for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
@@ -649,10 +647,11 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
   if (threadIdx.x == 0) *loss_out = total / ws->n_valid;
 }
 
-// In-place gradient scaling by a device scalar; a no-op when the scalar is exactly 1, except
-// for fp16, whose rows hold (softmax - onehot) * 2^15 * q / n_valid and are multiplied by
-// grad_output * 2^-15 / q (n_valid from the forward's workspace).
-// Ignored rows stay zero whatever the scalar is (torch's nll_loss backward leaves them 0).
+// The backward.  fp32 and bf16: in-place gradient scaling by a device scalar, a no-op when the
+// scalar is exactly 1.  fp16 (deferred gradient): the logits are still the logits, and each
+// element becomes (exp(x - lse) - [j == target]) * (grad_output / n_valid), computed in fp32 and
+// rounded to fp16 once (lse from the forward's workspace).  Ignored rows are zero whatever the
+// scalar is (torch's nll_loss backward leaves them 0).
 // The work items are (row, chunk of 1024 vectors or elements); a grid of up to 128 blocks
 // per CU walks them (a one-shot grid streams no faster and makes the common
 // grad_output == 1 launch several times dearer).  ALIGNED rows move 16-byte vectors (4 per
@@ -670,18 +669,21 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
                                                        const float* __restrict__ scale,
                                                        const CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
+  constexpr bool kDefer = std::is_same<T, _Float16>::value;
   float sc = *scale;
-  if constexpr (std::is_same<T, _Float16>::value) {
-    // power-of-two divisions: exact
-    sc = (sc * (1.0f / kF16GradScale)) / pow2_floor(ws->n_valid);
+  if constexpr (kDefer) {
+    sc = sc / ws->n_valid;  // grad_output / total_weight, as torch's nll_loss backward forms it
   } else {
     if (sc == 1.0f) return;
   }
+  const int64_t rows = items / chunks;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     const int64_t row = item / chunks;
     const int64_t c = item - row * chunks;
     const int64_t o = row / inner, ii = row - (row / inner) * inner;
-    if (ii >= valid_inner || targets[o * tos + ii * tis] == ignore_index) continue;
+    const int64_t tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
+    const bool skip = tgt == ignore_index;
+    if (!kDefer && skip) continue;
     T* p = logits + o * os + ii * is;
     // Unaligned rows: a head of elements before the first 16-byte boundary, a body of
     // 16-byte vectors and a tail of fewer than V elements; aligned rows are all body.
@@ -692,30 +694,46 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
     }
     const int nbody = (vocab - lead) / V;
     T* body = p + lead;
+    const float lse = (kDefer && !skip) ? row_lses(ws, rows)[row] : 0.0f;
+    // The gradient of element j (row index) holding x.
+    const auto grad = [&](float x, int64_t j) -> float {
+      if constexpr (kDefer) {
+        float y = exp_shifted(x, lse);
+        if (j == tgt) y -= 1.0f;
+        return y * sc;
+      } else {
+        return x * sc;
+      }
+    };
 #pragma unroll
     for (int k = 0; k < kScaleVecs; ++k) {
       const int64_t vi = c * (256 * kScaleVecs) + static_cast<int64_t>(k) * 256 + threadIdx.x;
       if (vi < nbody) {
         float x[V];
-        load_f32<T, true, true>(body + vi * V, x, V);
+        if (skip) {  // deferred gradient of an ignored row: zeros, nothing to read
 #pragma unroll
-        for (int i = 0; i < V; ++i) x[i] *= sc;
+          for (int i = 0; i < V; ++i) x[i] = 0.0f;
+        } else {
+          load_f32<T, true, true>(body + vi * V, x, V);
+#pragma unroll
+          for (int i = 0; i < V; ++i) x[i] = grad(x[i], lead + vi * V + i);
+        }
         store_f32<T, true, true>(body + vi * V, x, V);
       }
     }
     if constexpr (!ALIGNED) {
       if (c == 0) {
-        // The product is rounded to fp32 before the conversion, as in the vector path (left
-        // alone, the compiler fuses multiply and fp16 conversion into one rounding).
-        const auto scaled = [sc](T v) {
-          float y = Elem<T>::to_f32(v) * sc;
+        // The value is rounded to fp32 before the conversion, as in the vector path (left
+        // alone, the compiler fuses the last multiply and the fp16 conversion into one rounding).
+        const auto fix = [&](T v, int64_t j) {
+          float y = skip ? 0.0f : grad(Elem<T>::to_f32(v), j);
           asm volatile("" : "+v"(y));
           return Elem<T>::from_f32(y);
         };
         const int t = static_cast<int>(threadIdx.x);
-        if (t < lead) p[t] = scaled(p[t]);
+        if (t < lead) p[t] = fix(p[t], t);
         const int tail = lead + nbody * V + t;
-        if (t < V && tail < vocab) p[tail] = scaled(p[tail]);
+        if (t < V && tail < vocab) p[tail] = fix(p[tail], tail);
       }
     }
   }
@@ -841,12 +859,13 @@ int ce_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_
   const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
                        (outer <= 1 || (d.os * esize) % 16 == 0) &&
                        (inner <= 1 || (d.is * esize) % 16 == 0);
+  const int mode = !write_grad ? kGradNone : (dtype == PT_FLOAT16 ? kGradDefer : kGradWrite);
   if (dtype == PT_FLOAT32) {
-    dispatch_rows<float>(aligned, d, write_grad, ws, rows, st);
+    dispatch_rows<float>(aligned, d, mode, ws, rows, st);
   } else if (dtype == PT_FLOAT16) {
-    dispatch_rows<_Float16>(aligned, d, write_grad, ws, rows, st);
+    dispatch_rows<_Float16>(aligned, d, mode, ws, rows, st);
   } else {
-    dispatch_rows<__bf16>(aligned, d, write_grad, ws, rows, st);
+    dispatch_rows<__bf16>(aligned, d, mode, ws, rows, st);
   }
   if (int rc = check_launch(fn)) return rc;
   hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(kThreads), 0, st, ws, rows, loss_out);
@@ -921,7 +940,7 @@ extern "C" {
 
 size_t pt_cross_entropy_workspace_bytes(int64_t rows) {
   if (rows < 0) return 0;
-  return kHeader + static_cast<size_t>(rows) * sizeof(float);
+  return kHeader + 2 * static_cast<size_t>(rows) * sizeof(float);
 }
 
 int32_t* pt_cross_entropy_status(void* workspace) {

@@ -16,11 +16,10 @@ backward instead of reading wrong values; a plain read of the tensor after the l
 logging) would see the gradient.  ``inplace=False`` keeps the logits (the gradient then goes
 to a copy), and is the default of ``CrossEntropyWithFallback``, the drop-in for
 ``F.cross_entropy``.  Logits whose rows overlap in memory (e.g. an expanded tensor) are
-refused when the gradient would be written into them.  fp16 logits hold
-(softmax - onehot) * 2^15 * q / n_valid between the forward and the backward (q the largest
-power of two not above n_valid), which multiplies by grad_output * 2^-15 / q: the loss
-scale of fp16 training arrives only with the backward, and softmax / n_valid would mostly
-be below fp16's smallest subnormal.  The gradient buffer is
+refused when the gradient would be written into them.  fp16 logits keep their values until
+the backward, which writes (softmax - onehot) * grad_output / n_valid over them, rounded to
+fp16 once: the loss scale of fp16 training arrives only with the backward, and
+softmax / n_valid would mostly be below fp16's smallest subnormal.  The gradient buffer is
 consumed by the backward, so a second backward through the same graph raises.
 
 ``shift=True`` takes the language model's whole (B, S, V) logits and the (B, S) input ids

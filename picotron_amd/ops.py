@@ -406,9 +406,9 @@ def cross_entropy_scale_grad(
     workspace: Tensor | None = None,
 ) -> None:
     """dlogits *= grad_output in place (skipped on device when grad_output == 1).  For fp16
-    the rows hold (softmax - onehot) * 2^15 * q / n_valid (q: the largest power of two not
-    above n_valid) and ``workspace`` (the forward's) supplies n_valid:
-    dlogits *= grad_output * 2^-15 / q."""
+    the forward left the logits unchanged and this call writes the gradient,
+    (softmax - onehot) * grad_output / n_valid rounded once, from the row log-sum-exps and
+    n_valid in ``workspace`` (the forward's)."""
 
     device = _check_cuda(dlogits, targets, grad_output)
     outer, inner, os_, is_, vocab = ce_rows(dlogits)

@@ -55,7 +55,7 @@ def test_workspace_queries():
     # 3 rows: the element-wise path (2 rows per 8-wave block) needs 2 partial rows
     assert lib.pt_rmsnorm_bwd_workspace_bytes(3, 128, _lib.PT_FLOAT32) == 2 * 128 * 4
     assert lib.pt_rmsnorm_bwd_workspace_bytes(0, 128, _lib.PT_FLOAT32) == 0
-    assert lib.pt_cross_entropy_workspace_bytes(8192) == 16 + 8192 * 4
+    assert lib.pt_cross_entropy_workspace_bytes(8192) == 16 + 8192 * 8  # row losses + row lse
     assert lib.pt_adamw_block_elems() == 1024
 
 
