@@ -20,17 +20,35 @@ from picotron_amd import _lib, ops
 _DISABLED_ENV = "PICOTRON_HIP_DISABLE"
 
 
-def require_hip(exc: type[RuntimeError], op: str, *tensors: Tensor) -> None:
+# The process-wide parts of the gate are constants to torch.compile: it evaluates them once
+# while tracing and keeps the answer, so a compiled model neither re-checks them per call nor
+# breaks its graph at the ctypes and environment lookups.
+
+
+@torch.compiler.assume_constant_result
+def _process_reason() -> str:
+    """'' if the fused kernels may run in this process, else why not ('{op}' is a placeholder)."""
+
     if os.environ.get(_DISABLED_ENV, "") not in ("", "0"):
-        raise exc(f"HIP {op} disabled by {_DISABLED_ENV}.")
+        return "HIP {op} disabled by " + _DISABLED_ENV + "."
     reason = _lib.unavailable_reason()
-    if reason is not None:
-        raise exc(f"HIP kernel library unavailable: {reason}")
+    return "" if reason is None else "HIP kernel library unavailable: " + reason
+
+
+@torch.compiler.assume_constant_result
+def _device_supported(index: int) -> bool:
+    return ops.device_supported(index)
+
+
+def require_hip(exc: type[RuntimeError], op: str, *tensors: Tensor) -> None:
+    reason = _process_reason()
+    if reason:
+        raise exc(reason.replace("{op}", op))
     for t in tensors:
         if not t.is_cuda:
             raise exc(f"HIP {op} requires GPU tensors.")
     index = tensors[0].device.index
     if index is None:
         index = torch.cuda.current_device()
-    if not ops.device_supported(index):
+    if not _device_supported(index):
         raise exc(f"HIP {op} requires a gfx950 (MI355X) device.")

@@ -55,6 +55,15 @@ def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _compiling() -> bool:
+    """True while torch.compile traces: the launchers then record themselves as the custom
+    ops registered at the end of this module (opaque to the compiler, with fake
+    implementations for shape propagation) instead of calling the library; at run time the
+    compiled graph calls those ops, which call the launchers eagerly."""
+
+    return torch.compiler.is_compiling()
+
+
 @functools.lru_cache(maxsize=None)
 def device_supported(index: int) -> bool:
     """True if CUDA/HIP device ``index`` is a gfx950 GPU the library was built for."""
@@ -89,6 +98,8 @@ def _as_rows(t: Tensor, cols: int) -> Tensor:
 def rmsnorm_fwd(x: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
     """y = x * rsqrt(mean(x^2) + eps) * weight over the last dim; returns (y, rstd fp32)."""
 
+    if _compiling():
+        return torch.ops.picotron_amd.rmsnorm_fwd(x, weight, float(eps))
     device = _check_cuda(x, weight)
     cols = x.size(-1)
     if weight.dim() != 1 or weight.numel() != cols:
@@ -118,6 +129,9 @@ def rmsnorm_bwd(
 ) -> tuple[Tensor | None, Tensor | None]:
     """Gradients of RMSNorm w.r.t. x (x's dtype) and weight (weight's dtype)."""
 
+    if _compiling():
+        dx, dw = torch.ops.picotron_amd.rmsnorm_bwd(dy, x, weight, rstd)
+        return (dx if need_dx else None), (dw if need_dw else None)
     device = _check_cuda(dy, x, weight, rstd)
     cols = x.size(-1)
     if dy.dtype != x.dtype:
@@ -154,6 +168,8 @@ def residual_rmsnorm_fwd(
     """h = x + residual (rounded to x's dtype) and y = RMSNorm(h) in one pass; returns
     (h, y, rstd fp32)."""
 
+    if _compiling():
+        return torch.ops.picotron_amd.residual_rmsnorm_fwd(x, residual, weight, float(eps))
     device = _check_cuda(x, residual, weight)
     cols = x.size(-1)
     if residual.shape != x.shape or residual.dtype != x.dtype:
@@ -189,6 +205,9 @@ def residual_rmsnorm_bwd(
     """dh = RMSNorm-backward(dy) + dh_in (in h's dtype) and the weight gradient.  ``out``
     (may be ``dh_in`` itself) receives dh when given."""
 
+    if _compiling() and out is None:
+        dh, dw = torch.ops.picotron_amd.residual_rmsnorm_bwd(dy, dh_in, h, weight, rstd)
+        return dh, (dw if need_dw else None)
     device = _check_cuda(dy, h, weight, rstd)
     cols = h.size(-1)
     if dy.dtype != h.dtype:
@@ -237,6 +256,8 @@ def _flat(t: Tensor) -> Tensor:
 def swiglu_fwd(gate: Tensor, up: Tensor) -> Tensor:
     """silu(gate) * up, elementwise, in gate's dtype."""
 
+    if _compiling():
+        return torch.ops.picotron_amd.swiglu_fwd(gate, up)
     device = _check_cuda(gate, up)
     if gate.shape != up.shape or gate.dtype != up.dtype:
         raise ValueError("SwiGLU gate and up must match in shape and dtype")
@@ -252,6 +273,9 @@ def swiglu_fwd(gate: Tensor, up: Tensor) -> Tensor:
 def swiglu_bwd(
     dout: Tensor, gate: Tensor, up: Tensor, need_dgate: bool = True, need_dup: bool = True
 ) -> tuple[Tensor | None, Tensor | None]:
+    if _compiling():
+        dg, du = torch.ops.picotron_amd.swiglu_bwd(dout, gate, up)
+        return (dg if need_dgate else None), (du if need_dup else None)
     device = _check_cuda(dout, gate, up)
     if dout.dtype != gate.dtype:
         dout = dout.to(gate.dtype)
@@ -290,6 +314,11 @@ def rope(
     Outputs are new tensors with the inputs' logical shape and memory layout.
     """
 
+    if _compiling():
+        if x1 is None:
+            return torch.ops.picotron_amd.rope(x0, cos, sin, layout, bool(inverse)), None
+        y0, y1 = torch.ops.picotron_amd.rope_pair(x0, x1, cos, sin, layout, bool(inverse))
+        return y0, y1
     device = _check_cuda(x0, cos, sin) if x1 is None else _check_cuda(x0, x1, cos, sin)
     if layout not in LAYOUTS:
         raise ValueError(f"layout must be one of {sorted(LAYOUTS)}")
@@ -658,3 +687,100 @@ def copy_bytes(src: Tensor, dst: Tensor) -> None:
     if dst.numel() * dst.element_size() != nbytes or not src.is_contiguous() or not dst.is_contiguous():
         raise ValueError("copy_bytes needs contiguous tensors of equal byte size")
     _lib.call("pt_copy", src.data_ptr(), dst.data_ptr(), nbytes, _stream(device))
+
+
+# ------------------------------------------------------------------ torch.compile
+#
+# The launchers of the ops a compiled model contains (RMSNorm, the residual add + norm, SwiGLU,
+# RoPE) as custom operators: torch.compile records a call as one opaque node (no graph break
+# at the ctypes call) and propagates shapes through the fake implementations; the compiled
+# graph calls the launcher eagerly.  Every output is a new tensor.  The cross-entropy and the
+# optimizer step run outside picotron's compiled model (train_loop.py:136-168) and keep only
+# their eager path.
+
+
+@torch.library.custom_op("picotron_amd::rmsnorm_fwd", mutates_args=())
+def _op_rmsnorm_fwd(x: Tensor, weight: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    return rmsnorm_fwd(x, weight, eps)
+
+
+@_op_rmsnorm_fwd.register_fake
+def _(x, weight, eps):
+    return x.new_empty(x.shape), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("picotron_amd::rmsnorm_bwd", mutates_args=())
+def _op_rmsnorm_bwd(dy: Tensor, x: Tensor, weight: Tensor, rstd: Tensor) -> tuple[Tensor, Tensor]:
+    return rmsnorm_bwd(dy, x, weight, rstd)
+
+
+@_op_rmsnorm_bwd.register_fake
+def _(dy, x, weight, rstd):
+    return x.new_empty(x.shape), weight.new_empty((x.size(-1),))
+
+
+@torch.library.custom_op("picotron_amd::residual_rmsnorm_fwd", mutates_args=())
+def _op_residual_rmsnorm_fwd(
+    x: Tensor, residual: Tensor, weight: Tensor, eps: float
+) -> tuple[Tensor, Tensor, Tensor]:
+    return residual_rmsnorm_fwd(x, residual, weight, eps)
+
+
+@_op_residual_rmsnorm_fwd.register_fake
+def _(x, residual, weight, eps):
+    return x.new_empty(x.shape), x.new_empty(x.shape), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("picotron_amd::residual_rmsnorm_bwd", mutates_args=())
+def _op_residual_rmsnorm_bwd(
+    dy: Tensor, dh_in: Tensor | None, h: Tensor, weight: Tensor, rstd: Tensor
+) -> tuple[Tensor, Tensor]:
+    return residual_rmsnorm_bwd(dy, dh_in, h, weight, rstd)
+
+
+@_op_residual_rmsnorm_bwd.register_fake
+def _(dy, dh_in, h, weight, rstd):
+    return h.new_empty(h.shape), weight.new_empty((h.size(-1),))
+
+
+@torch.library.custom_op("picotron_amd::swiglu_fwd", mutates_args=())
+def _op_swiglu_fwd(gate: Tensor, up: Tensor) -> Tensor:
+    return swiglu_fwd(gate, up)
+
+
+@_op_swiglu_fwd.register_fake
+def _(gate, up):
+    return gate.new_empty(gate.shape)
+
+
+@torch.library.custom_op("picotron_amd::swiglu_bwd", mutates_args=())
+def _op_swiglu_bwd(dout: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
+    return swiglu_bwd(dout, gate, up)
+
+
+@_op_swiglu_bwd.register_fake
+def _(dout, gate, up):
+    return gate.new_empty(gate.shape), up.new_empty(up.shape)
+
+
+@torch.library.custom_op("picotron_amd::rope", mutates_args=())
+def _op_rope(x: Tensor, cos: Tensor, sin: Tensor, layout: str, inverse: bool) -> Tensor:
+    return rope(x, cos, sin, layout=layout, inverse=inverse)[0]
+
+
+@_op_rope.register_fake
+def _(x, cos, sin, layout, inverse):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("picotron_amd::rope_pair", mutates_args=())
+def _op_rope_pair(
+    x0: Tensor, x1: Tensor, cos: Tensor, sin: Tensor, layout: str, inverse: bool
+) -> tuple[Tensor, Tensor]:
+    y0, y1 = rope(x0, cos, sin, layout=layout, inverse=inverse, x1=x1)
+    return y0, y1
+
+
+@_op_rope_pair.register_fake
+def _(x0, x1, cos, sin, layout, inverse):
+    return torch.empty_like(x0), torch.empty_like(x1)

@@ -185,6 +185,24 @@ def test_rmsnorm_add_and_norm_cpu_fallback():
     torch.testing.assert_close(y, RMSNorm(8, eps=1e-6)(x + r), rtol=0, atol=0)
 
 
+def test_compiled_modules_fall_back_like_eager_on_cpu():
+    """Under torch.compile the launch gate still rejects CPU tensors, and the modules take
+    their PyTorch path in one graph, with the same values as eagerly."""
+
+    torch._dynamo.reset()
+    torch.manual_seed(6)
+    norm = RMSNorm(16, use_triton_rmsnorm=True)
+    mlp = SwiGLU(16, 32, use_triton_swiglu=True)
+    x = torch.randn(3, 16)
+    with pytest.warns(RuntimeWarning, match="requires GPU tensors"):
+        expected = mlp(norm(x))
+    model = torch.nn.Sequential(norm, mlp)
+    explained = torch._dynamo.explain(model)(x)
+    assert explained.graph_break_count == 0
+    torch._dynamo.reset()
+    torch.testing.assert_close(torch.compile(model, backend="aot_eager")(x), expected)
+
+
 def test_adamw_clip_fallback_is_clip_grad_norm_then_step():
     torch.manual_seed(4)
     ref_params = [torch.nn.Parameter(torch.randn(5)), torch.nn.Parameter(torch.randn(3, 2))]
