@@ -233,7 +233,8 @@ int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq
  *    first block index}
  * where "first block index" is the running sum of ceil(numel / pt_adamw_block_elems())
  * over the preceding records (so record 0 has 0); total_blocks is the sum over all
- * records.  Every record must have numel >= 1.
+ * records.  Every record must have numel >= 1 (a call with more records than blocks is
+ * refused with PT_EINVAL), and total_blocks is at most 2^24.
  * Replaces triton_adamw_step / AdamWStepWithFallback
  * (src/picotron/nn/triton_kernels/adamw.py:14-47), which always raises today, and the
  * torch.optim.AdamW step it falls back to (src/picotron/training/train_loop.py:308-325). */

@@ -49,16 +49,44 @@ struct AdamScalars {
   float eps;
 };
 
+// The record whose blocks include block `blk`: the last i with table[i].first_block <= blk
+// (first_block increases from 0 along the table).  A kSearchWays-way search: each round
+// loads its probes' first_block values together (independent scalar loads, one wait), so a
+// table of n records costs about log17(n) dependent rounds instead of a binary search's
+// log2(n): one round up to 17 records, two up to 273, three up to 4369.
+// Every round shrinks [lo, hi] (lo rises or hi falls), so the loop ends on any table.
+// Block indexes and record counts are below 2^24 (checked before every launch), so the
+// search runs in 32 bits and reads the low word of each first_block.
+constexpr int kSearchWays = 16;
+
+__device__ __forceinline__ uint32_t first_block_of(const AdamRec* __restrict__ table, uint32_t i) {
+  return *reinterpret_cast<const uint32_t*>(&table[i].first_block);
+}
+
 __device__ __forceinline__ int64_t find_tensor(const AdamRec* __restrict__ table, int64_t ntensors,
-                                               int64_t blk) {
-  int64_t lo = 0, hi = ntensors - 1;
+                                               int64_t block) {
+  const uint32_t blk = static_cast<uint32_t>(block);
+  uint32_t lo = 0, hi = static_cast<uint32_t>(ntensors - 1);
   while (lo < hi) {
-    const int64_t mid = (lo + hi + 1) / 2;
-    if (table[mid].first_block <= blk) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
+    // probe k at lo + ceil((k + 1) * len / kSearchWays): nondecreasing, in (lo, hi], and
+    // every index of (lo, hi] when len <= kSearchWays (the last round)
+    const uint32_t len = hi - lo;
+    uint32_t fb[kSearchWays];
+#pragma unroll
+    for (int k = 0; k < kSearchWays; ++k)
+      fb[k] = first_block_of(table, lo + ((k + 1) * len + kSearchWays - 1) / kSearchWays);
+    uint32_t new_lo = lo, new_hi = hi;
+#pragma unroll
+    for (int k = kSearchWays - 1; k >= 0; --k) {
+      const uint32_t probe = lo + ((k + 1) * len + kSearchWays - 1) / kSearchWays;
+      if (fb[k] <= blk) {
+        if (probe > new_lo) new_lo = probe;
+      } else {
+        new_hi = probe - 1;  // the loop runs downward: ends at the first probe past blk
+      }
     }
+    lo = new_lo;
+    hi = new_hi;
   }
   return lo;
 }
@@ -166,9 +194,16 @@ struct BlockSpan {
   bool vec;  // a whole 16-byte-aligned block: one float4 per thread
 };
 
+// `row` carries the record of the previous block of the same walk step (-1 for the first):
+// consecutive blocks stay in that record or move on by one, since every record has a block.
 __device__ __forceinline__ BlockSpan block_span(const AdamRec* __restrict__ table,
-                                                int64_t ntensors, int64_t vb) {
-  const AdamRec r = table[find_tensor(table, ntensors, vb)];
+                                                int64_t ntensors, int64_t vb, int64_t& row) {
+  if (row < 0) {
+    row = find_tensor(table, ntensors, vb);
+  } else {
+    while (row + 1 < ntensors && table[row + 1].first_block <= vb) ++row;
+  }
+  const AdamRec r = table[row];
   BlockSpan b;
   b.g = as_global<float>(r.g);
   b.start = (vb - r.first_block) * kBlockElems;
@@ -190,13 +225,14 @@ __global__ __launch_bounds__(kThreads) void grad_stats_kernel(const AdamRec* __r
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWalkUnroll; base < nblocks; base += step) {
     BlockSpan sp[kWalkUnroll];
     f32x4 gv[kWalkUnroll];
+    int64_t row = -1;
 #pragma unroll
     for (int u = 0; u < kWalkUnroll; ++u) {
       sp[u].g = nullptr;
       sp[u].vec = false;
       sp[u].start = sp[u].end = 0;
       if (base + u < nblocks) {
-        sp[u] = block_span(table, ntensors, base + u);
+        sp[u] = block_span(table, ntensors, base + u, row);
         if (sp[u].vec)
           gv[u] = __builtin_nontemporal_load(
               reinterpret_cast<gptr<const f32x4>>(sp[u].g + sp[u].start + threadIdx.x * 4));
@@ -292,13 +328,14 @@ __global__ __launch_bounds__(kThreads) void grad_scale_kernel(const AdamRec* __r
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * kWalkUnroll; base < nblocks; base += step) {
     BlockSpan sp[kWalkUnroll];
     f32x4 gv[kWalkUnroll];
+    int64_t row = -1;
 #pragma unroll
     for (int u = 0; u < kWalkUnroll; ++u) {
       sp[u].g = nullptr;
       sp[u].vec = false;
       sp[u].start = sp[u].end = 0;
       if (base + u < nblocks) {
-        sp[u] = block_span(table, ntensors, base + u);
+        sp[u] = block_span(table, ntensors, base + u, row);
         if (sp[u].vec)
           gv[u] = __builtin_nontemporal_load(
               reinterpret_cast<gptr<const f32x4>>(sp[u].g + sp[u].start + threadIdx.x * 4));
@@ -366,6 +403,9 @@ int check_table(const char* fn, const int64_t* table, int64_t n_tensors, int64_t
     return fail(PT_EINVAL, name + ": table not 8-byte aligned");
   if (total_blocks * kThreads > 0xffffffffLL)
     return fail(PT_EUNSUPPORTED, name + ": more than 2^24 blocks in one launch");
+  if (n_tensors > total_blocks)
+    return fail(PT_EINVAL, name + ": more records than blocks (every record needs a block; "
+                                  "leave empty tensors out of the table)");
   return PT_OK;
 }
 

@@ -70,6 +70,9 @@ def test_workspace_queries():
         ("pt_adamw_step", (None, 1, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
         ("pt_adamw_step_device_step", (None, 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
         ("pt_adamw_step_device_step", (ctypes.addressof(_HOST_TABLE), 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
+        # more records than blocks: a record without a block (an empty tensor) is refused
+        ("pt_adamw_step", (ctypes.addressof(_HOST_TABLE), 2, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
+        ("pt_grad_scale", (ctypes.addressof(_HOST_TABLE), 3, 2, None, None), _lib.PT_EINVAL),
         ("pt_copy", (None, None, 16, None), _lib.PT_EINVAL),
         ("pt_cross_entropy", (None, 4, 1, 8, 0, 8, None, 1, 0, -100, None, 0, None, 0, 7, None), _lib.PT_EINVAL),
         ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EINVAL),

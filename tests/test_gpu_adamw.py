@@ -67,6 +67,64 @@ def test_matches_torch_adamw_multi_tensor(gpu):
     assert sd["state"][0]["step"].device.type == "cpu" and float(sd["state"][0]["step"]) == 4.0
 
 
+def _many_sizes(count: int, seed: int) -> list[int]:
+    """Sizes that put record boundaries everywhere: single elements, exactly one 1024-element
+    block, one block and one element, and larger tensors, shuffled."""
+
+    rng = np.random.default_rng(seed)
+    base = [1, 2, 1023, 1024, 1025, 2048, 4096, 5000, 65_536, 300_001]
+    return [int(x) for x in rng.permutation(np.resize(base, count))]
+
+
+@pytest.mark.parametrize("count", [17, 300, 1500])
+def test_many_tensors_find_their_blocks(gpu, count):
+    """One launch over hundreds of tensors: every block must find its own record (a search
+    over the table of several rounds), for the step and for the fused clip's walks."""
+
+    from picotron_amd.nn.triton_kernels import triton_clip_grad_norm_and_step
+
+    sizes = _many_sizes(count, count)
+    print(f"many tensors: {count} records, {sum(sizes)} elements", flush=True)
+    fused = [torch.nn.Parameter(randn((n,), torch.float32, gpu, 7 * i, 0.02)) for i, n in enumerate(sizes)]
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in fused]
+    opt_f = torch.optim.AdamW(fused, **HP)
+    opt_r = torch.optim.AdamW(ref, foreach=False, **HP)
+    for step in range(2):
+        for i, (a, b) in enumerate(zip(fused, ref)):
+            g = randn(a.shape, torch.float32, gpu, 1000 * step + i, 1e-3)
+            a.grad, b.grad = g, g.clone()
+        if step == 0:
+            triton_adamw_step(opt_f)
+        else:
+            ref_total = torch.nn.utils.clip_grad_norm_(ref, 0.05)
+            total = triton_clip_grad_norm_and_step(opt_f, 0.05)
+            close_fp32(total.reshape(()), ref_total.reshape(()))
+        opt_r.step()
+    for a, b in zip(fused, ref):
+        close_fp32(a.detach(), b.detach())
+        close_fp32(a.grad, b.grad)
+        close_fp32(opt_f.state[a]["exp_avg"], opt_r.state[b]["exp_avg"])
+        close_fp32(opt_f.state[a]["exp_avg_sq"], opt_r.state[b]["exp_avg_sq"])
+
+
+def test_many_tensors_zero_clip_scales_every_gradient(gpu):
+    """The ZeRO clip's in-place scaling walk over 300 tensors: every gradient scaled once."""
+
+    from picotron_amd.nn.triton_kernels import triton_zero_clip_grad_norm_
+
+    sizes = _many_sizes(300, 5)
+    params = [torch.nn.Parameter(torch.zeros(n, device=gpu)) for n in sizes]
+    grads = [randn((n,), torch.float32, gpu, 3 * i + 1, 1e-3) for i, n in enumerate(sizes)]
+    for p, g in zip(params, grads):
+        p.grad = g.clone()
+    norm = torch.linalg.vector_norm(torch.cat([g.double() for g in grads]))
+    total = triton_zero_clip_grad_norm_(params, 0.01)
+    close_fp32(total.double().reshape(()), norm)
+    coef = 0.01 / (float(total) + 1e-6)
+    for p, g in zip(params, grads):
+        close_fp32(p.grad, g * coef)
+
+
 def test_param_groups_late_group_and_fused_clip(gpu):
     # Several groups with their own hyperparameters, a group added after two steps (its
     # parameters count their own steps: one launch per distinct step value), a parameter
