@@ -367,6 +367,97 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
 }
 
+// Forward without a gradient write (no gradient, or the fp16 deferred one) over 16-byte
+// aligned rows: a read-only pass, so nothing of the row has to stay in registers and
+// 256-thread workgroups (about 40 VGPRs) share a CU several at a time, each streaming its
+// own row; the register-resident kernel, one 1024-thread workgroup per CU, leaves the CU's
+// loads idle while it reduces a row when there is no store phase to overlap.  Per thread,
+// batches of kLseBatch 16-byte nontemporal loads (raw buffer loads: the range check returns
+// zeros past the row, masked to -inf here) feed an online max / sum-exp with one rescale
+// per batch; the wave and block reductions are those of ce_rows_kernel.  Thread 0 reads
+// the target logit at the start (in flight with the row) and writes the row loss and, for a
+// deferred gradient, the row's log-sum-exp.
+constexpr int kLseThreads = 256;
+constexpr int kLseWaves = kLseThreads / 64;
+constexpr int kLseBatch = 8;
+
+template <typename T>
+__global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
+    const T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
+    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
+  constexpr int V = Elem<T>::VEC;
+  __shared__ float red_m[kLseWaves];
+  __shared__ float red_s[kLseWaves];
+  const int tid = threadIdx.x;
+  const int wave = tid / 64, lane = tid % 64;
+  const int64_t row = blockIdx.x;
+  const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
+  if (cur.skip) {
+    if (tid == 0) row_losses(ws)[row] = 0.0f;
+    return;
+  }
+  const T* p = logits + cur.off;
+  const bool bad = cur.tgt < 0 || cur.tgt >= vocab;
+  float xt = NAN;  // a target outside [0, vocab): NaN loss and status bit 0
+  if (tid == 0) {
+    if (bad) {
+      atomicOr(&ws->status, 1);
+    } else {
+      xt = Elem<T>::to_f32(p[cur.tgt]);
+    }
+  }
+  const int row_bytes = vocab * static_cast<int>(sizeof(T));
+  const int nvec = row_bytes / 16;
+  const auto buf = row_buffer(const_cast<T*>(p), row_bytes);
+  float m = -INFINITY, s = 0.0f;
+  for (int base = tid; base < nvec; base += kLseThreads * kLseBatch) {
+    Vec16<T> v[kLseBatch];
+#pragma unroll
+    for (int u = 0; u < kLseBatch; ++u)
+      v[u].raw = __builtin_amdgcn_raw_buffer_load_b128(buf, (base + u * kLseThreads) * 16, 0,
+                                                       kNonTemporal);
+    float cm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kLseBatch; ++u) {
+      if (base + u * kLseThreads >= nvec) {
+        const uint32_t ninf = kNegInfWord<T>;
+        v[u].raw = u32x4{ninf, ninf, ninf, ninf};
+      }
+#pragma unroll
+      for (int i = 0; i < V; ++i) cm = fmaxf(cm, Elem<T>::to_f32(v[u].e[i]));
+    }
+    const float nm = fmaxf(m, cm);
+    const float ref = nm == -INFINITY ? 0.0f : nm;
+    float add = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kLseBatch; ++u) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) add += exp_shifted(Elem<T>::to_f32(v[u].e[i]), ref);
+    }
+    s = s * exp_shifted(m, ref) + add;
+    m = nm;
+  }
+  const float mw = wave_max(m);
+  const float sw = wave_sum(s * exp_shifted(m, mw == -INFINITY ? 0.0f : mw));
+  if (lane == 0) {
+    red_m[wave] = mw;
+    red_s[wave] = sw;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float M = red_m[0];
+#pragma unroll
+    for (int w = 1; w < kLseWaves; ++w) M = fmaxf(M, red_m[w]);
+    const float refM = M == -INFINITY ? 0.0f : M;
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kLseWaves; ++w) S += red_s[w] * exp_shifted(red_m[w], refM);
+    row_losses(ws)[row] = row_loss(M, S, xt);
+    if (write_grad == kGradDefer) row_lses(ws, gridDim.x)[row] = M + __logf(S);
+  }
+}
+
 // Rows that the register-resident kernel does not take -- longer than it holds, or not
 // 16-byte aligned -- with row_bytes + kStreamBatchBytes < 2^31: one 1024-thread workgroup
 // per row in two passes.  A row is split into a head of up to V-1 elements before its first
@@ -677,10 +768,24 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
     if (sc == 1.0f) return;
   }
   const int64_t rows = items / chunks;
+  // Item decode in 32 bits when the counts allow it (the usual case; a uniform branch):
+  // 64-bit divisions are long scalar sequences ahead of every item's loads.
+  const bool small = items <= 0xffffffffLL && inner <= 0xffffffffLL;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    const int64_t row = item / chunks;
-    const int64_t c = item - row * chunks;
-    const int64_t o = row / inner, ii = row - (row / inner) * inner;
+    int64_t row, c, o, ii;
+    if (small) {
+      const uint32_t r32 = static_cast<uint32_t>(item) / static_cast<uint32_t>(chunks);
+      const uint32_t o32 = r32 / static_cast<uint32_t>(inner);
+      row = r32;
+      c = static_cast<uint32_t>(item) - r32 * static_cast<uint32_t>(chunks);
+      o = o32;
+      ii = r32 - o32 * static_cast<uint32_t>(inner);
+    } else {
+      row = item / chunks;
+      c = item - row * chunks;
+      o = row / inner;
+      ii = row - o * inner;
+    }
     const int64_t tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
     const bool skip = tgt == ignore_index;
     if (!kDefer && skip) continue;
@@ -694,7 +799,9 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
     }
     const int nbody = (vocab - lead) / V;
     T* body = p + lead;
-    const float lse = (kDefer && !skip) ? row_lses(ws, rows)[row] : 0.0f;
+    // read whether or not the row is ignored (an ignored row's value is never used), so the
+    // load does not wait for the target's
+    const float lse = kDefer ? row_lses(ws, rows)[row] : 0.0f;
     // The gradient of element j (row index) holding x.
     const auto grad = [&](float x, int64_t j) -> float {
       if constexpr (kDefer) {
@@ -705,22 +812,49 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
         return x * sc;
       }
     };
+    // The item's chunk of the body through a raw buffer resource sized to the part of the
+    // chunk inside the row: loads past it return zeros and stores past it are dropped, so
+    // the code has no branches, all four loads are in flight together and every gradient
+    // is computed before the first store (a load waited for after a store waits for the
+    // store too).  Within a row, indexes fit in 32 bits.
+    const int cstart = static_cast<int>(c) * (256 * kScaleVecs);  // first vector of the chunk
+    const int cvecs = nbody - cstart < 256 * kScaleVecs ? nbody - cstart : 256 * kScaleVecs;
+    const int cbytes = cvecs > 0 ? cvecs * 16 : 0;
+    T* cptr = body + static_cast<int64_t>(cstart) * V;
+    // an ignored row (deferred gradient) reads nothing: its load resource is empty
+    const auto lbuf = row_buffer(cptr, skip ? 0 : cbytes);
+    const auto sbuf = row_buffer(cptr, cbytes);
+    // the target's index in the chunk, or -1 when it is not there (ignored, in another
+    // chunk, in the head or tail of an unaligned row, or outside the row)
+    const int64_t trel64 = tgt - lead - static_cast<int64_t>(cstart) * V;
+    const int trel = (trel64 >= 0 && trel64 < int64_t{256} * kScaleVecs * V) ? static_cast<int>(trel64) : -1;
+    const int tid = static_cast<int>(threadIdx.x);
+    Vec16<T> in[kScaleVecs];
+#pragma unroll
+    for (int k = 0; k < kScaleVecs; ++k)
+      in[k].raw = __builtin_amdgcn_raw_buffer_load_b128(lbuf, (k * 256 + tid) * 16, 0, kNonTemporal);
+    Vec16<T> out[kScaleVecs];
 #pragma unroll
     for (int k = 0; k < kScaleVecs; ++k) {
-      const int64_t vi = c * (256 * kScaleVecs) + static_cast<int64_t>(k) * 256 + threadIdx.x;
-      if (vi < nbody) {
-        float x[V];
-        if (skip) {  // deferred gradient of an ignored row: zeros, nothing to read
 #pragma unroll
-          for (int i = 0; i < V; ++i) x[i] = 0.0f;
+      for (int i = 0; i < V; ++i) {
+        float y;
+        if constexpr (kDefer) {
+          y = exp_shifted(Elem<T>::to_f32(in[k].e[i]), lse);
+          if ((k * 256 + tid) * V + i == trel) y -= 1.0f;
+          y = skip ? 0.0f : y * sc;
         } else {
-          load_f32<T, true, true>(body + vi * V, x, V);
-#pragma unroll
-          for (int i = 0; i < V; ++i) x[i] = grad(x[i], lead + vi * V + i);
+          y = Elem<T>::to_f32(in[k].e[i]) * sc;
         }
-        store_f32<T, true, true>(body + vi * V, x, V);
+        // rounded to fp32 and then to the storage type, as torch rounds (left alone, the
+        // compiler fuses the multiply and the 16-bit conversion into one rounding)
+        asm volatile("" : "+v"(y));
+        out[k].e[i] = Elem<T>::from_f32(y);
       }
     }
+#pragma unroll
+    for (int k = 0; k < kScaleVecs; ++k)
+      __builtin_amdgcn_raw_buffer_store_b128(out[k].raw, sbuf, (k * 256 + tid) * 16, 0, kNonTemporal);
     if constexpr (!ALIGNED) {
       if (c == 0) {
         // The value is rounded to fp32 before the conversion, as in the vector path (left
@@ -778,6 +912,14 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
                    hipStream_t st) {
   const int64_t per_thread = (static_cast<int64_t>(d.vocab) + int64_t{kThreads} * Elem<T>::VEC - 1) /
                              (int64_t{kThreads} * Elem<T>::VEC);
+  const int64_t row_bytes = static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T));
+  if (aligned && write_grad != kGradWrite &&
+      row_bytes + int64_t{kLseThreads} * kLseBatch * 16 < (int64_t{1} << 31)) {
+    hipLaunchKernelGGL(ce_lse_kernel<T>, dim3(static_cast<unsigned>(rows)), dim3(kLseThreads), 0,
+                       st, static_cast<const T*>(d.logits), d.inner, d.valid_inner, d.os, d.is,
+                       d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
+    return;
+  }
   if (aligned) {
 #define PT_CE_CASE(N)                                  \
   if (per_thread <= N) {                               \
@@ -880,11 +1022,23 @@ void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, co
   constexpr int64_t kChunk = 256 * Elem<T>::VEC * kScaleVecs;
   const int64_t chunks = (d.vocab + kChunk - 1) / kChunk;
   const int64_t items = rows * chunks;
-  const int64_t cap = static_cast<int64_t>(num_cus()) * 128;
+  // fp32 / bf16 scaling: a walk of up to 128 workgroups per CU, at most 4 resident per CU
+  // (four 16-byte vectors in flight per thread: [8192, 128256] bf16 761 -> 714 us, vocab
+  // 151936 935 -> 846 us); a one-shot grid streams no faster and makes the common
+  // grad_output == 1 launch, which returns at once, several times dearer.  fp16 (the deferred
+  // gradient, always computed): one workgroup per item, at most 3 resident per CU, so that no
+  // item's loads wait behind an earlier item's stores in the same wave ([4 x 2049, 128256]
+  // 711 -> 659 us against the walk; 4 per CU 685 us, 2 per CU 791 us).  The grid stays below
+  // 2^24 workgroups (the walk covers any remainder).  PT_CE_SCALE_BLOCKS_PER_CU,
+  // PT_CE_SCALE_OCCUPANCY and PT_CE_DEFER_OCCUPANCY override the three figures.
+  constexpr bool kDefer = std::is_same<T, _Float16>::value;
+  static const int64_t walk_blocks = env_int("PT_CE_SCALE_BLOCKS_PER_CU", 128);
+  const int64_t cap = (kDefer || walk_blocks <= 0) ? (int64_t{1} << 24) - 1
+                                                   : static_cast<int64_t>(num_cus()) * walk_blocks;
   const unsigned grid = static_cast<unsigned>(items < cap ? items : cap);
-  // At most 4 resident workgroups per CU (four 16-byte vectors in flight per thread):
-  // [8192, 128256] bf16 761 -> 714 us, vocab 151936 935 -> 846 us.
-  static const int per_cu = static_cast<int>(env_int("PT_CE_SCALE_OCCUPANCY", 4));
+  static const int walk_per_cu = static_cast<int>(env_int("PT_CE_SCALE_OCCUPANCY", 4));
+  static const int defer_per_cu = static_cast<int>(env_int("PT_CE_DEFER_OCCUPANCY", 3));
+  const int per_cu = kDefer ? defer_per_cu : walk_per_cu;
   const auto kernel = ce_scale_kernel<T, ALIGNED>;
   size_t lds = occupancy_lds(per_cu, 0);
   if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;

@@ -29,6 +29,17 @@ def _grad_close(grad, ref, n_valid, dtype):
     torch.testing.assert_close(grad.double() * n_valid, ref.double() * n_valid, rtol=rtol, atol=atol)
 
 
+def _loss_only_streams(logits, dtype) -> bool:
+    """Whether the loss-only forward takes the read-only streaming kernel, while a forward
+    that writes the gradient takes another one: 16-byte-aligned rows."""
+
+    es = logits.element_size()
+    rows_aligned = all(
+        (st * es) % 16 == 0 for st, n in zip(logits.stride()[:-1], logits.shape[:-1]) if n > 1
+    )
+    return logits.data_ptr() % 16 == 0 and (logits.size(-1) * es) % 16 == 0 and rows_aligned
+
+
 def _check(logits, targets, dtype):
     ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
     n_valid = int((targets != -100).sum())
@@ -36,7 +47,13 @@ def _check(logits, targets, dtype):
     assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
     buf = logits.clone()
     loss2, ws = ops.cross_entropy(buf, targets, write_grad=True)
-    assert loss2.item() == loss.item()  # the loss does not depend on writing the gradient
+    if dtype == torch.float16 or not _loss_only_streams(logits, dtype):
+        # the same kernel with and without the gradient (fp16 defers it to the backward)
+        assert loss2.item() == loss.item()
+    else:
+        # fp32 / bf16: the kernel that writes the gradient in place against the read-only
+        # streaming pass of the loss alone: the same sum in another order
+        assert abs(loss2.item() - loss.item()) <= 1e-6 * abs(loss.item())
     assert ops.cross_entropy_status(ws) == 0
     if dtype == torch.float16:
         # the fp16 forward leaves the logits alone; the backward writes the gradient.  A
