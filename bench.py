@@ -803,7 +803,7 @@ class CrossEntropyTrainFp16Workload(CrossEntropyTrainWorkload):
         rows = b * s
         self.bytes_per_step = 3 * rows * v * 2 + 16 * rows  # forward: read; backward: read + write
         self.dominant = ("shifted cross-entropy fp16 forward + autograd backward (ce_prepare_kernel + "
-                         "ce_rows_kernel + ce_finish_kernel, then ce_scale_kernel writing the gradient)")
+                         "ce_lse_kernel + ce_finish_kernel, then ce_scale_kernel writing the gradient)")
         self.dominant_bytes = self.bytes_per_step
         self.description = (
             f"train-loop loss on fp16 model logits [{b}, {s}, {v}] ~N(0,2^2) against input_ids[:, 1:] "
