@@ -60,29 +60,31 @@ def _check_group(group: dict) -> None:
         raise _reject("tensor-valued betas")
 
 
-def _check_param(p: Tensor) -> None:
-    if not p.is_cuda or not p.grad.is_cuda:
+def _check_param(p: Tensor, g: Tensor) -> None:
+    if not p.is_cuda or not g.is_cuda:
         raise _reject("CPU tensors")
-    if p.dtype != torch.float32 or p.grad.dtype != torch.float32:
+    if p.dtype != torch.float32 or g.dtype != torch.float32:
         raise _reject(f"{p.dtype} parameters")
-    if p.grad.is_sparse:
+    if g.is_sparse:
         raise _reject("sparse gradients")
-    if not p.is_contiguous() or not p.grad.is_contiguous() or p.grad.device != p.device:
+    if not p.is_contiguous() or not g.is_contiguous() or g.device != p.device:
         raise _reject("non-contiguous parameters or gradients")
 
 
-def _check_state(state: dict, p: Tensor) -> None:
+def _check_state(state: dict, p: Tensor, capturable: bool = False) -> None:
     """An existing optimizer state (resumed from a checkpoint, or written by torch's own step)
     must be what the kernel's raw pointers assume: fp32 contiguous moments of p's size on p's
-    device and a one-element step tensor.  ``Optimizer.load_state_dict`` does not check state
-    shapes, and torch's step would raise on a mismatch where the kernel would read and write
-    out of bounds."""
+    device and a one-element step tensor (for a capturable group an fp32 scalar on p's
+    device).  ``Optimizer.load_state_dict`` does not check state shapes, and torch's step
+    would raise on a mismatch where the kernel would read and write out of bounds."""
 
     if len(state) == 0:
         return
     step = state.get("step")
     if not isinstance(step, Tensor) or step.numel() != 1:
         raise _reject("optimizer states whose step is not a one-element tensor")
+    if capturable and (step.device != p.device or step.dtype != torch.float32):
+        raise _reject("capturable steps that are not fp32 scalars on the parameter's device")
     for key in ("exp_avg", "exp_avg_sq"):
         m = state.get(key)
         if not isinstance(m, Tensor):
@@ -109,7 +111,7 @@ def _device_table(host_table: Tensor, device: torch.device) -> Tensor:
     tensors, as in the usual warm-up before a capture): building it there would need a
     pinned host allocation and a host-to-device copy inside the graph."""
 
-    key = (device, tuple(host_table.flatten().tolist()))
+    key = (device, host_table.numpy().tobytes())
     cached = _table_cache.pop(key, None)
     capturing = torch.cuda.is_current_stream_capturing()
     if cached is None:
@@ -134,21 +136,24 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
         raise _reject(f"{type(optimizer).__name__} (only torch.optim.AdamW)")
     groups = []
     device = None
+    state_of = optimizer.state
     for group in optimizer.param_groups:
         _check_group(group)
-        params = [p for p in group["params"] if p.grad is not None]
-        for p in params:
-            _check_state(optimizer.state.get(p, {}), p)
-            _check_param(p)
+        capturable = bool(group.get("capturable", False))
+        params = []
+        for p in group["params"]:
+            g = p.grad
+            if g is None:
+                continue
+            state = state_of.get(p)
+            if state:
+                _check_state(state, p, capturable)
+            _check_param(p, g)
             if device is None:
                 device = p.device
             elif p.device != device:
                 raise _reject("parameters on several devices")
-            if group.get("capturable", False) and len(optimizer.state[p]) != 0:
-                step = optimizer.state[p]["step"]
-                if (not isinstance(step, Tensor) or step.device != p.device
-                        or step.dtype != torch.float32 or step.numel() != 1):
-                    raise _reject("capturable steps that are not fp32 scalars on the parameter's device")
+            params.append(p)
         groups.append((group, params))
     if device is None:
         return groups, None
@@ -181,13 +186,15 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
 
     launches = []
     created = []
+    state_of = optimizer.state
     for group, params in groups:
         if not params:
             continue
         beta1, beta2 = group["betas"]
         capturable = bool(group.get("capturable", False))
+        states = []
         for p in params:
-            state = optimizer.state[p]
+            state = state_of[p]
             if len(state) == 0:
                 if capturable:
                     state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
@@ -196,33 +203,42 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
                 state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                 state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                 created.append(p)
+            states.append(state)
         hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
                      weight_decay=group["weight_decay"])
         if capturable:
             # the step values stay on the device: no host read, one launch for the group
-            buckets = [(None, params)]
+            buckets = [(None, params, states)]
         else:
-            by_step: dict[float, list[Tensor]] = {}
-            for p in params:
-                # the value `state["step"] += 1` leaves in the float32 tensor
-                step = float(np.float32(optimizer.state[p]["step"].item()) + np.float32(1.0))
-                by_step.setdefault(step, []).append(p)
-            buckets = list(by_step.items())
-        for step, ps in buckets:
-            grads = [p.grad for p in ps]
-            exp_avgs = [optimizer.state[p]["exp_avg"] for p in ps]
-            exp_avg_sqs = [optimizer.state[p]["exp_avg_sq"] for p in ps]
-            host_table, total_blocks = ops.adamw_table(ps, grads, exp_avgs, exp_avg_sqs)
+            # one launch per distinct step count (usually one for the whole group); the value
+            # is the one `state["step"] += 1` leaves in the float32 tensor
+            values = [state["step"].item() for state in states]
+            if values.count(values[0]) == len(values):
+                buckets = [(_next_step(values[0]), params, states)]
+            else:
+                by_step: dict[float, tuple[list, list]] = {}
+                for p, state, value in zip(params, states, values):
+                    ps, sts = by_step.setdefault(_next_step(value), ([], []))
+                    ps.append(p)
+                    sts.append(state)
+                buckets = [(step, ps, sts) for step, (ps, sts) in by_step.items()]
+        for step, ps, sts in buckets:
+            host_table, total_blocks = ops.adamw_table(
+                ps, [p.grad for p in ps], [st["exp_avg"] for st in sts],
+                [st["exp_avg_sq"] for st in sts])
             if total_blocks == 0:
                 continue
             table = _device_table(host_table, device)
             if step is None:
-                steps = _device_table(
-                    ops.adamw_step_table(ps, [optimizer.state[p]["step"] for p in ps]), device)
+                steps = _device_table(ops.adamw_step_table(ps, [st["step"] for st in sts]), device)
                 launches.append((table, total_blocks, steps, hyper))
             else:
                 launches.append((table, total_blocks, None, dict(hyper, step=step)))
     return launches, created
+
+
+def _next_step(value: float) -> float:
+    return float(np.float32(value) + np.float32(1.0))
 
 
 def _launch(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | None,
@@ -230,14 +246,12 @@ def _launch(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | N
     """Advances every stepped parameter's step counter (as torch's AdamW does: on the host,
     or for a capturable group on the device) and launches the prepared updates."""
 
+    state_of = optimizer.state
     for group, params in groups:
-        if not params:
-            continue
-        if group.get("capturable", False):
-            torch._foreach_add_([optimizer.state[p]["step"] for p in params], 1.0)
-        else:
-            for p in params:
-                optimizer.state[p]["step"] += 1
+        if params:
+            # float32 step tensors on the host, or on the device for a capturable group: one
+            # call adds 1 to all of them, the same float32 addition as `step += 1` on each
+            torch._foreach_add_([state_of[p]["step"] for p in params], 1.0)
     for table, total_blocks, steps, hyper in launches:
         if steps is not None:
             ops.adamw_step_device_step(table, total_blocks, steps, grad_scale=grad_scale,

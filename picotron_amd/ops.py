@@ -12,6 +12,7 @@ from __future__ import annotations
 import ctypes
 import functools
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -514,21 +515,26 @@ def adamw_block_elems() -> int:
     return int(_lib.lib().pt_adamw_block_elems())
 
 
+@functools.lru_cache(maxsize=None)
+def _adamw_block_elems() -> int:
+    return adamw_block_elems()
+
+
 def adamw_table(
     params: list[Tensor], grads: list[Tensor], exp_avgs: list[Tensor], exp_avg_sqs: list[Tensor]
 ) -> tuple[Tensor, int]:
     """Host int64 [n, 6] table for :func:`adamw_step` and its total block count."""
 
-    per = adamw_block_elems()
+    per = _adamw_block_elems()
     rows = []
     first = 0
     for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs):
         n = p.numel()
         if n == 0:
             continue
-        rows.append([p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), n, first])
+        rows += (p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), n, first)
         first += (n + per - 1) // per
-    table = torch.tensor(rows, dtype=torch.int64) if rows else torch.empty((0, 6), dtype=torch.int64)
+    table = torch.from_numpy(np.array(rows, dtype=np.int64).reshape(-1, 6))
     return table, first
 
 
@@ -585,7 +591,7 @@ def adamw_step_table(params: list[Tensor], steps: list[Tensor]) -> Tensor:
     of :func:`adamw_table` (which skips empty parameters)."""
 
     addrs = [s.data_ptr() for p, s in zip(params, steps) if p.numel() > 0]
-    return torch.tensor(addrs, dtype=torch.int64) if addrs else torch.empty(0, dtype=torch.int64)
+    return torch.from_numpy(np.array(addrs, dtype=np.int64))
 
 
 def adamw_step_device_step(
