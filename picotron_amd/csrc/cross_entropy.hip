@@ -920,7 +920,11 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
                        d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
     return;
   }
-  if (aligned) {
+  // fp16 never writes its gradient in the forward (it is deferred to the backward): its
+  // aligned rows take ce_lse_kernel above (or, from 2 GB, the stream kernel), so the
+  // register-resident kernel has no fp16 instances.
+  if constexpr (!std::is_same<T, _Float16>::value) {
+    if (aligned) {
 #define PT_CE_CASE(N)                                  \
   if (per_thread <= N) {                               \
     launch_rows<T, N>(d, write_grad, ws, rows, st);    \
@@ -937,6 +941,7 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
     PT_CE_CASE(14)
     PT_CE_CASE(16)
 #undef PT_CE_CASE
+    }
   }
   if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
       (int64_t{1} << 31)) {
