@@ -2,10 +2,11 @@
 SwiGLU compiles into ONE graph (the launchers are custom operators, opaque to the compiler),
 its compiled forward and backward launch the HIP kernels, and they match the eager modules.
 
-picotron compiles nothing itself; a user who wraps its model in torch.compile reaches these
-ops through the same modules (reference src/picotron/models/picotron_decoder.py:20-46,
-src/picotron/nn/feedforward.py:13-43).  The backend is "aot_eager": it traces forward and
-backward through AOTAutograd and runs the graphs eagerly, so the test needs no code generator.
+A model wrapped in torch.compile reaches these ops through the same modules (reference src/picotron/models/picotron_decoder.py:20-46,
+src/picotron/nn/feedforward.py:13-43), and picotron's `compile_model` option does so itself.
+The main test uses the "aot_eager" backend: it traces forward and backward through
+AOTAutograd and runs the graphs eagerly, so it needs no code generator; the last one uses the
+default backend, as that option does.
 """
 
 from __future__ import annotations
@@ -99,3 +100,31 @@ def test_block_compiles_to_one_graph_and_matches_eager(gpu, monkeypatch, dtype, 
     for name in grads_e:
         check(grads_c[name], grads_e[name])
 
+
+
+def test_block_compiles_with_the_default_backend(gpu, monkeypatch):
+    """picotron's own `compile_model` option calls torch.compile(model) with the default
+    backend (reference src/picotron/training/train_loop.py:230-241): the fused ops stay calls
+    into the library inside the generated code.  fp32, where the code generator's fused
+    elementwise ops round as eager does up to the last bits."""
+
+    print("compile block, default backend, fp32", flush=True)
+    torch._dynamo.reset()
+    torch.manual_seed(0)
+    eager = _Block("rotate_half").to(gpu, torch.float32)
+    compiled_model = copy.deepcopy(eager)
+    x = randn((2, 64, HIDDEN), torch.float32, gpu, 3)
+    dy = randn((2, 64, HIDDEN), torch.float32, gpu, 4)
+    compiled = torch.compile(compiled_model, fullgraph=True)
+    counts = _count_launches(monkeypatch)
+    out_c, dx_c, grads_c = _run(compiled, x, dy, compiled_model)
+    torch.cuda.synchronize()
+    for fn, n in [("pt_rmsnorm_fwd", 1), ("pt_residual_rmsnorm_fwd", 1), ("pt_swiglu_fwd", 1),
+                  ("pt_swiglu_bwd", 1), ("pt_residual_rmsnorm_bwd", 1), ("pt_rope", 2),
+                  ("pt_rmsnorm_bwd", 1)]:
+        assert counts.get(fn, 0) == n, (fn, counts)
+    out_e, dx_e, grads_e = _run(eager, x, dy)
+    close_fp32(out_c, out_e)
+    close_fp32(dx_c, dx_e)
+    for name in grads_e:
+        close_fp32(grads_c[name], grads_e[name])
