@@ -839,7 +839,23 @@ class CrossEntropyTrainFp16Workload(CrossEntropyTrainWorkload):
         return {"torch_autocast_fp16_ms_per_step": round(sec * 1e3, 4)}
 
     def cpu_baseline(self) -> dict:
-        return None
+        from oracle import cross_entropy as o_ce
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        s = 257
+        logits = self.leaf.detach()[:, :s].cpu()
+        ids = self.ids[:, :s].cpu()
+        sec, calls = _time_cpu(lambda: o_ce.fallback_forward_backward(
+            logits[:, :-1, :].transpose(1, 2), ids[:, 1:]))
+        rows = self.b * s
+        return dict(
+            value=(3 * rows * self.vocab * 2 + 16 * rows) / sec / 1e9, unit="GB/s", cores=cores, kind="port",
+            sample=f"first {s} positions of each sequence, fp16 logits: F.cross_entropy fwd + autograd bwd on "
+                   f"the fp32 upcast of the sliced view (the reference fallback under fp16 autocast), median "
+                   f"of {calls} calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=self.b * (s - 1) / sec,
+        )
 
 
 class AdamWWorkload(Workload):
