@@ -478,8 +478,9 @@ def test_overlapping_rows_are_never_written_in_place(gpu):
 )
 def test_fp16_gradient_is_written_by_the_backward(gpu, vocab, offset, grad_output):
     """fp16: the forward leaves the logits alone and keeps each row's log-sum-exp; the
-    backward writes (softmax - onehot) * grad_output / n_valid rounded once, on register-resident
-    and batched rows, aligned and not (row starts shifted by an element offset), with targets at
+    backward writes (softmax - onehot) * grad_output / n_valid rounded once, on aligned rows
+    (the read-only streaming forward) and unaligned ones (row starts shifted by an element
+    offset: the batched forward), short and long, with targets at
     both ends of the row and an ignored row; nothing outside the view is written."""
 
     rows = 12
