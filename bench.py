@@ -34,6 +34,7 @@ import time
 from pathlib import Path
 
 import torch
+from torch.nn import functional as F
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -1221,10 +1222,13 @@ class ModulesWorkload(Workload):
         for name, (rshape, sshape, dtype) in self.SHAPES.items():
             d = rshape[-1]
             norm = RMSNorm(d, eps=1e-5, use_triton_rmsnorm=True).to(device="cuda", dtype=dtype)
+            norm_ref = RMSNorm(d, eps=1e-5).to(device="cuda", dtype=dtype)
             with torch.no_grad():
                 norm.weight.copy_(_seeded((d,), dtype, 2, 0.02, 1.0))
+                norm_ref.weight.copy_(norm.weight)
             case = dict(
                 norm=norm,
+                norm_ref=norm_ref,
                 x=_seeded(rshape, dtype, 3).requires_grad_(True),
                 dy=_seeded(rshape, dtype, 4),
                 g=_seeded(sshape, dtype, 5).requires_grad_(True),
@@ -1291,6 +1295,17 @@ class ModulesWorkload(Workload):
         out = triton_swiglu(g, u)
         torch.autograd.grad(out, (g, u), case["ds"])
 
+    @staticmethod
+    def _fallback_call(case):
+        """The same calls on the reference's PyTorch path (the modules with their flags off:
+        the eager RMSNorm formula and ``F.silu(gate) * up``, autograd backwards)."""
+
+        norm, x, g, u = case["norm_ref"], case["x"], case["g"], case["u"]
+        y = norm(x)
+        torch.autograd.grad(y, (x, norm.weight), case["dy"])
+        out = F.silu(g) * u
+        torch.autograd.grad(out, (g, u), case["ds"])
+
     def step(self, events):
         case = self.cases["headline"]
         if events is not None:
@@ -1320,6 +1335,14 @@ class ModulesWorkload(Workload):
                 case["direct"]()
             torch.cuda.synchronize()
             t_direct = time.perf_counter() - t0
+            for _ in range(3):
+                self._fallback_call(case)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                self._fallback_call(case)
+            torch.cuda.synchronize()
+            t_fallback = time.perf_counter() - t0
             paths[name] = {
                 "rmsnorm_shape": list(case["x"].shape),
                 "swiglu_shape": list(case["g"].shape),
@@ -1328,6 +1351,7 @@ class ModulesWorkload(Workload):
                 "module_wall_us_per_call": round(t_module / reps * 1e6, 2),
                 "module_host_issue_us_per_call": round(t_issue / reps * 1e6, 2),
                 "direct_c_abi_wall_us_per_call": round(t_direct / reps * 1e6, 2),
+                "reference_fallback_wall_us_per_call": round(t_fallback / reps * 1e6, 2),
                 "module_gbs": round(case["bytes"] / (t_module / reps) / 1e9, 1),
                 "direct_gbs": round(case["bytes"] / (t_direct / reps) / 1e9, 1),
             }
