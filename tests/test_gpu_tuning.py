@@ -45,6 +45,10 @@ _SCRIPT = textwrap.dedent("""
     loss, ws = ops.cross_entropy(logits, targets, write_grad=True)
     ops.cross_entropy_scale_grad(logits, targets, torch.tensor(0.37, device=dev), workspace=ws)
     add(loss, logits)
+    logits16 = (randn(300, 32000) * 2).half()
+    loss16, ws16 = ops.cross_entropy(logits16, targets % 32000, write_grad=True)
+    ops.cross_entropy_scale_grad(logits16, targets % 32000, torch.tensor(4096.0, device=dev), workspace=ws16)
+    add(loss16, logits16)
     p = torch.nn.Parameter(randn(1 << 20, dtype=torch.float32))
     p.grad = randn(1 << 20, dtype=torch.float32)
     opt = torch.optim.AdamW([p], lr=1e-3, weight_decay=0.1)
@@ -56,7 +60,8 @@ _SCRIPT = textwrap.dedent("""
 
 _KNOBS = ("PT_ADAMW_BLOCKS_PER_CU", "PT_SWIGLU_FWD_OCCUPANCY", "PT_SWIGLU_BWD_OCCUPANCY",
           "PT_CE_SCALE_OCCUPANCY", "PT_CE_OCCUPANCY", "PT_ROPE_OCCUPANCY",
-          "PT_RMSNORM_FWD_OCCUPANCY", "PT_RMSNORM_BWD_OCCUPANCY")
+          "PT_RMSNORM_FWD_OCCUPANCY", "PT_RMSNORM_BWD_OCCUPANCY", "PT_CE_DEFER_OCCUPANCY",
+          "PT_CE_SCALE_BLOCKS_PER_CU")
 
 
 def _digest(env_values: dict[str, str]) -> str:
@@ -71,5 +76,5 @@ def _digest(env_values: dict[str, str]) -> str:
 
 def test_occupancy_limits_change_speed_only(gpu):
     unlimited = _digest({k: "0" for k in _KNOBS})
-    limited = _digest({k: v for k, v in zip(_KNOBS, ("2", "3", "1", "2", "1", "4", "5", "1"))})
+    limited = _digest({k: v for k, v in zip(_KNOBS, ("2", "3", "1", "2", "1", "4", "5", "1", "2", "8"))})
     assert unlimited == limited
