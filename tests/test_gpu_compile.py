@@ -128,3 +128,34 @@ def test_block_compiles_with_the_default_backend(gpu, monkeypatch):
     close_fp32(dx_c, dx_e)
     for name in grads_e:
         close_fp32(grads_c[name], grads_e[name])
+
+
+def test_fused_loss_inside_a_compiled_function(gpu):
+    """The fused cross-entropy is not a custom op: inside a compiled function the compiler
+    runs it eagerly (a graph break at its library calls) and the result is the eager one, with
+    no fallback to F.cross_entropy."""
+
+    import warnings
+
+    from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback
+
+    torch._dynamo.reset()
+    torch.manual_seed(1)
+    head = nn.Linear(64, 1000, bias=False).to(gpu)
+    x = randn((2, 33, 64), torch.float32, gpu, 5)
+    ids = torch.randint(0, 1000, (2, 33), generator=torch.Generator(device=gpu).manual_seed(6), device=gpu)
+    loss_fn = CrossEntropyWithFallback(use_triton=True, inplace=True)
+
+    def step(inp):
+        return loss_fn(head(inp), ids, shift=True)
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        loss_c = torch.compile(step, backend="aot_eager")(x)
+        loss_c.backward()
+        grad_c = head.weight.grad.clone()
+        head.weight.grad = None
+        loss_e = step(x)
+        loss_e.backward()
+    assert loss_c.item() == loss_e.item()
+    assert torch.equal(grad_c, head.weight.grad)
