@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
 
 // Forward without a gradient write (no gradient, or the fp16 deferred one) over 16-byte
 // aligned rows: a read-only pass, so nothing of the row has to stay in registers and
-// 256-thread workgroups (about 40 VGPRs) share a CU several at a time, each streaming its
+// 256-thread workgroups (46-73 VGPRs) share a CU six or more at a time, each streaming its
 // own row; the register-resident kernel, one 1024-thread workgroup per CU, leaves the CU's
 // loads idle while it reduces a row when there is no store phase to overlap.  Per thread,
 // batches of kLseBatch 16-byte nontemporal loads (raw buffer loads: the range check returns
