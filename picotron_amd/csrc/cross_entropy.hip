@@ -18,8 +18,10 @@
 //      element's gradient (softmax_t - 1) / n_valid comes from the exact fp32 target logit.
 //      Longer or unaligned rows use ce_rows_batched (two passes, batches of loads in flight,
 //      the second pass served largely by the Infinity Cache).
-//      Each row's fp32 loss goes to the workspace.  fp16 logits are left as they are: the
-//      row's log-sum-exp goes to the workspace instead, and the backward (ce_scale) writes the
+//      Each row's fp32 loss goes to the workspace.  When no gradient is written in the
+//      forward -- the loss alone, or fp16 logits, which are left as they are -- aligned rows
+//      take ce_lse instead: a read-only stream, 256-thread workgroups several to a CU, that
+//      also keeps the row's log-sum-exp for fp16, whose backward (ce_scale) then writes the
 //      gradient with grad_output applied, rounding to fp16 once.
 //   3. ce_finish: one block sums the per-row losses in a fixed order and divides by
 //      n_valid, so the loss is bitwise reproducible.
