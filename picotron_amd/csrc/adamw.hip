@@ -12,7 +12,7 @@
 // with step_size = lr / (1 - beta1^t) and bc2_sqrt = (1 - beta2^t)^0.5 computed in double
 // on the host, then rounded to fp32 as torch rounds Python scalars for fp32 tensors.
 //
-// One launch covers every tensor: block b finds its tensor by binary search over the
+// One launch covers every tensor: block b finds its tensor by a 16-way search over the
 // per-tensor first-block indices in the device table, then streams its chunk of
 // kBlockElems elements (16-byte vectors when all four pointers are aligned).
 //
