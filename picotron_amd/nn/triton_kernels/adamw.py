@@ -431,7 +431,10 @@ def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float |
     host read of the finite flag, as ``grad_scaler.step`` makes; then the AdamW step applies the
     multiplier as it reads each gradient and writes the unscaled, clipped gradient back.  When a
     gradient is inf or NaN the step is skipped (no state is created or advanced), the gradients
-    are left unscaled as ``unscale_`` leaves them, and the scaler backs off exactly as torch's:
+    are left unscaled as ``unscale_`` leaves them (with ``max_norm``, torch's
+    ``clip_grad_norm_`` would then also multiply them by a coefficient computed from the
+    non-finite norm, zero or NaN; here they are not clipped, and the next ``zero_grad`` discards
+    them either way), and the scaler backs off exactly as torch's:
     the flag is recorded in the scaler's per-optimizer state as ``unscale_`` records it, and
     ``grad_scaler.update()`` consumes it.  Returns True when the step was skipped.
 
