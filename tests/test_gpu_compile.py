@@ -4,9 +4,9 @@ its compiled forward and backward launch the HIP kernels, and they match the eag
 
 A model wrapped in torch.compile reaches these ops through the same modules (reference src/picotron/models/picotron_decoder.py:20-46,
 src/picotron/nn/feedforward.py:13-43), and picotron's `compile_model` option does so itself.
-The main test uses the "aot_eager" backend: it traces forward and backward through
-AOTAutograd and runs the graphs eagerly, so it needs no code generator; the last one uses the
-default backend, as that option does.
+Most tests use the "aot_eager" backend: it traces forward and backward through AOTAutograd
+and runs the graphs eagerly, so it needs no code generator; one uses the default backend, as
+that option does.
 """
 
 from __future__ import annotations
@@ -101,7 +101,6 @@ def test_block_compiles_to_one_graph_and_matches_eager(gpu, monkeypatch, dtype, 
         check(grads_c[name], grads_e[name])
 
 
-
 def test_block_compiles_with_the_default_backend(gpu, monkeypatch):
     """picotron's own `compile_model` option calls torch.compile(model) with the default
     backend (reference src/picotron/training/train_loop.py:230-241): the fused ops stay calls
@@ -159,3 +158,59 @@ def test_fused_loss_inside_a_compiled_function(gpu):
         loss_e.backward()
     assert loss_c.item() == loss_e.item()
     assert torch.equal(grad_c, head.weight.grad)
+
+
+def test_compiled_decoder_trains_like_eager(gpu, monkeypatch):
+    """The reference's own compile check (tests/test_torch_compile.py:30-49: three training
+    steps of a compiled model give the eager losses within rtol 1e-5, atol 1e-6) on a small
+    decoder with every fused kernel on: the model compiled, the fused loss and the fused
+    clip + AdamW step outside it, as the train loop has them (train_loop.py:136-168).  The
+    compiled model's weights then load unchanged into the same decoder on the PyTorch
+    fallbacks (tests/test_torch_compile.py:52-71)."""
+
+    import warnings
+
+    from test_gpu_decoder_step import VOCAB, Decoder, _models
+    from picotron_amd.nn.triton_kernels import AdamWStepWithFallback, CrossEntropyWithFallback
+
+    torch._dynamo.reset()
+    _, eager = _models(gpu)
+    compiled_model = copy.deepcopy(eager)
+    compiled = torch.compile(compiled_model, backend="aot_eager")
+    batches = [torch.randint(0, VOCAB, (2, 65), generator=torch.Generator().manual_seed(40 + i)).to(gpu)
+               for i in range(3)]
+
+    def train(model, params):
+        optimizer = torch.optim.AdamW(params, lr=2e-3, betas=(0.9, 0.95), weight_decay=0.1)
+        loss_fn = CrossEntropyWithFallback(use_triton=True, inplace=True)
+        stepper = AdamWStepWithFallback(use_triton=True)
+        losses = []
+        for ids in batches:
+            optimizer.zero_grad(set_to_none=True)
+            loss = loss_fn(model(ids), ids, shift=True)
+            loss.backward()
+            stepper.step(optimizer, max_grad_norm=1.0)
+            losses.append(loss.item())
+        return losses
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)  # a fallback would warn
+        eager_losses = train(eager, list(eager.parameters()))
+        counts = _count_launches(monkeypatch)
+        compiled_losses = train(compiled, list(compiled_model.parameters()))
+    # per step: 2 blocks' input norms + the final norm, 2 residual norms, 2 SwiGLUs, 2 RoPE
+    # launches per block forward and backward, the shifted loss, the clip and the step
+    for fn, n in [("pt_rmsnorm_fwd", 3), ("pt_rmsnorm_bwd", 3), ("pt_residual_rmsnorm_fwd", 2),
+                  ("pt_residual_rmsnorm_bwd", 2), ("pt_swiglu_fwd", 2), ("pt_swiglu_bwd", 2),
+                  ("pt_rope", 4), ("pt_cross_entropy_shifted", 1), ("pt_clip_grad_norm", 1),
+                  ("pt_adamw_step_scaled", 1)]:
+        assert counts.get(fn, 0) == 3 * n, (fn, counts)
+    print(f"eager losses {eager_losses} compiled {compiled_losses}", flush=True)
+    torch.testing.assert_close(torch.tensor(compiled_losses), torch.tensor(eager_losses),
+                               rtol=1e-5, atol=1e-6)
+    assert compiled_losses[-1] < compiled_losses[0]
+
+    portable = Decoder(fused=False).to(gpu)
+    portable.load_state_dict(compiled_model.state_dict())
+    for name, value in compiled_model.state_dict().items():
+        assert torch.equal(portable.state_dict()[name], value), name
