@@ -163,15 +163,19 @@ __device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t v
   return true;
 }
 
-// Row loss lse - x_t, written (max - x_t) + ln(sum exp(x - max)): exact when the target is
-// the row max and free of the cancellation of two large numbers.
+// Row loss lse - x_t, written (max - x_t) + ln(sum exp(x - max)), free of the cancellation
+// of two large numbers (lse and x_t): max - x_t is exact when the target is within a factor
+// of two of the max, and a dominant target's small loss ln(sum) carries only the rounding of
+// the fp32 sum, a few units of 2^-24.
 __device__ __forceinline__ float row_loss(float mx, float se, float xt) {
   return (mx - xt) + __logf(se);
 }
 
 // Gradient of the target element, (softmax_t - 1) / n_valid, from the exact fp32 target
-// logit as exp(x_t - max) / sum: when softmax_t is close to 1 the difference x_t - max is
-// small and exact, so the result keeps fp32's relative accuracy (exactly 0 for one class).
+// logit as exp(x_t - max) / sum - 1 (exactly 0 for one class).  For a dominant target the
+// subtraction cancels: the result is then accurate to a few units of 2^-24 absolutely, the
+// rounding of the fp32 sum, not relative to its own small size (torch's fp32 path,
+// exp(log_softmax_t) - 1, cancels the same way).
 __device__ __forceinline__ float target_grad(float mx, float se, float xt, float inv_n) {
   return (exp_shifted(xt, mx) / se - 1.0f) * inv_n;
 }

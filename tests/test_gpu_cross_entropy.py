@@ -18,6 +18,13 @@ pytestmark = pytest.mark.gpu
 
 LOSS_RTOL = 1e-4  # fp32-accumulated loss vs the fp64 oracle
 
+# fp32 target entries softmax_t - 1 (the negative entries of the gradient): for a dominant
+# target the difference cancels, and its error is that of softmax_t rounded near 1, a few
+# units of 2^-24, not relative to the small difference (torch's fp32 exp(log_softmax_t) - 1
+# cancels the same way).  Observed up to 8.4e-8 over 2200 random shapes (vocab 2 rows, where
+# targets often dominate); the bound is 8 units.
+TARGET_ATOL_FP32 = 2.0**-21
+
 
 def _grad_close(grad, ref, n_valid, dtype):
     # d loss/d logits = (softmax - onehot) / n_valid: compare (softmax - onehot) so the
@@ -26,7 +33,16 @@ def _grad_close(grad, ref, n_valid, dtype):
     # test_fp16_gradients_at_training_scale.)
     rtol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
     atol = {torch.float32: 1e-9, torch.float16: 2.0**-25 * n_valid + 1e-9, torch.bfloat16: 1e-7}[dtype]
-    torch.testing.assert_close(grad.double() * n_valid, ref.double() * n_valid, rtol=rtol, atol=atol)
+    a, e = grad.double() * n_valid, ref.double() * n_valid
+    if dtype == torch.float32 and e.numel() > 0:
+        tol = rtol * e.abs() + torch.where(e < 0, TARGET_ATOL_FP32, atol)
+        excess = (a - e).abs() - tol
+        worst = int(excess.argmax())
+        assert float(excess.flatten()[worst]) <= 0, (
+            f"fp32 gradient entry {worst}: {float(a.flatten()[worst])} against "
+            f"{float(e.flatten()[worst])} (tolerance {float(tol.flatten()[worst])})")
+    else:
+        torch.testing.assert_close(a, e, rtol=rtol, atol=atol)
 
 
 def _loss_only_streams(logits, dtype) -> bool:
@@ -61,7 +77,10 @@ def _check(logits, targets, dtype):
         # softmax / n_valid is mostly below fp16's subnormals in the reference as well):
         # relative bound with a floor of one fp16 subnormal step, independent of n_valid
         assert torch.equal(buf, logits)
-        g = 65536.0
+        # GradScaler's initial 2^16, halved for a single valid row, whose target entry
+        # (softmax_t - 1) * g would otherwise round past fp16's largest finite value (in
+        # torch's path as well: GradScaler would then back off)
+        g = 65536.0 if n_valid > 1 else 32768.0
         ops.cross_entropy_scale_grad(buf, targets, torch.full((), g, device=logits.device), workspace=ws)
         ref = ref_grad.to(buf.device) * g
         excess = (buf.double() - ref).abs() - (2e-3 * ref.abs() + 2.0 ** -24)
