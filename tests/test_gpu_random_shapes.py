@@ -90,12 +90,18 @@ def test_rope_random(gpu, case):
     layout = ["interleaved", "rotate_half"][rng.integers(2)]
     dtype = DTYPES[rng.integers(3)]
     extra = int(rng.integers(0, 3))  # table rows beyond the sequence
-    print(f"rope case {case}: b {b} s {s} hq {hq} hk {hk} d {d} {layout} {dtype}", flush=True)
+    bshd = bool(rng.integers(4))  # mostly attention's view, sometimes contiguous (B, H, S, D)
+    print(f"rope case {case}: b {b} s {s} hq {hq} hk {hk} d {d} {layout} {dtype} "
+          f"{'(B,S,H,D) memory' if bshd else 'contiguous'}", flush=True)
     seed = 4000 + 2 * case
     cos, sin = o_rope.tables(s + extra, d, 500_000.0, device=gpu)
-    # (B, H, S, D) views of (B, S, H, D) memory, as attention produces them
-    q = randn((b, s, hq, d), dtype, gpu, seed).transpose(1, 2)
-    k = randn((b, s, hk, d), dtype, gpu, seed + 1).transpose(1, 2)
+    if bshd:
+        # (B, H, S, D) views of (B, S, H, D) memory, as attention produces them
+        q = randn((b, s, hq, d), dtype, gpu, seed).transpose(1, 2)
+        k = randn((b, s, hk, d), dtype, gpu, seed + 1).transpose(1, 2)
+    else:
+        q = randn((b, hq, s, d), dtype, gpu, seed)
+        k = randn((b, hk, s, d), dtype, gpu, seed + 1)
     yq, yk = ops.rope(q, cos, sin, layout=layout, x1=k)
     close(yq, o_rope.rotate(q, cos, sin, layout), dtype)
     close(yk, o_rope.rotate(k, cos, sin, layout), dtype)
@@ -120,6 +126,49 @@ def test_cross_entropy_random(gpu, case):
     if not bool((targets != -100).any()):
         targets[0] = 0
     t_ce._check(logits, targets, dtype)
+
+
+@pytest.mark.parametrize("case", range(CASES // 2))
+def test_cross_entropy_train_loop_view_random(gpu, case):
+    """The train loop's own call, F.cross_entropy(logits[:, :-1, :].transpose(1, 2),
+    input_ids[:, 1:]) (reference train_loop.py:141-144): (B, V, S - 1) views whose class
+    dimension is contiguous and whose rows are V apart; the gradient lands in the view and
+    the last position of the buffer is left alone."""
+
+    rng = _rng("ce_view", case)
+    b = int(rng.integers(1, 4))
+    s = _log_uniform(rng, 2, 300)
+    v = _log_uniform(rng, 1, 150_000)
+    dtype = DTYPES[rng.integers(3)]
+    print(f"train-loop view cross-entropy case {case}: b {b} s {s} v {v} {dtype}", flush=True)
+    seed = 8000 + case
+    base = randn((b, s, v), dtype, gpu, seed, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(seed + 1)
+    ids = torch.randint(0, v, (b, s), generator=g, device=gpu)
+    ids[torch.rand((b, s), generator=g, device=gpu) < 0.1] = -100
+    targets = ids[:, 1:]
+    if not bool((targets != -100).any()):
+        ids[0, 1] = 0
+    view = base[:, :-1, :].transpose(1, 2)
+    ref_loss, ref_grad = t_ce.o_ce.forward_backward(view, targets)
+    n_valid = int((targets != -100).sum())
+    loss, _ = ops.cross_entropy(view, targets)
+    assert abs(loss.item() - ref_loss.item()) <= t_ce.LOSS_RTOL * abs(ref_loss.item())
+    buf = base.clone()
+    bview = buf[:, :-1, :].transpose(1, 2)
+    loss2, ws = ops.cross_entropy(bview, targets, write_grad=True)
+    assert abs(loss2.item() - ref_loss.item()) <= t_ce.LOSS_RTOL * abs(ref_loss.item())
+    assert ops.cross_entropy_status(ws) == 0
+    if dtype == torch.float16:
+        # the backward writes the fp16 gradient at a GradScaler-sized scale (as in _check)
+        scale = 65536.0 if n_valid > 1 else 32768.0
+        ops.cross_entropy_scale_grad(bview, targets, torch.full((), scale, device=gpu), workspace=ws)
+        ref = ref_grad.to(gpu) * scale
+        excess = (bview.double() - ref).abs() - (2e-3 * ref.abs() + 2.0 ** -24)
+        assert float(excess.max()) <= 0, f"fp16 gradient: max excess {float(excess.max())}"
+    else:
+        t_ce._grad_close(bview, ref_grad, n_valid, dtype)
+    assert torch.equal(buf[:, -1, :], base[:, -1, :])
 
 
 @pytest.mark.parametrize("case", range(CASES // 2))
