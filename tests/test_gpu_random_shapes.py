@@ -2,7 +2,7 @@
 counts and hidden sizes off the tuned grid, odd vocabularies, strided and offset views, long
 parameter lists.  Each case prints its parameters first, so a failure names it.  The checks
 are the per-family ones of the other parity tests (same tolerances).  PT_RANDOM_CASES sets the
-number of cases per family (default 40; some families run half as many)."""
+number of cases per family (default 100; some families run half as many)."""
 
 from __future__ import annotations
 
@@ -24,7 +24,7 @@ from picotron_amd.nn.triton_kernels import triton_adamw_step, triton_clip_grad_n
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
-CASES = int(os.environ.get("PT_RANDOM_CASES", "40"))
+CASES = int(os.environ.get("PT_RANDOM_CASES", "100"))
 
 
 def _rng(family: str, case: int) -> np.random.Generator:
