@@ -870,8 +870,8 @@ class AdamWWorkload(Workload):
         n = self.n
         self.p = _seeded((n,), torch.float32, 110, 0.02)
         self.g = _seeded((n,), torch.float32, 111, 1e-3)
-        self.m = torch.zeros(n, dtype=torch.float32, device="cuda")
-        self.v = torch.zeros(n, dtype=torch.float32, device="cuda")
+        # the moments as the fused optimizer creates them (ops.adamw_moments: one allocation)
+        ((self.m, self.v),) = ops.adamw_moments([self.p])
         host, blocks = ops.adamw_table([self.p], [self.g], [self.m], [self.v])
         self.table = host.cuda()
         self.blocks = blocks
@@ -881,8 +881,9 @@ class AdamWWorkload(Workload):
         self.dominant = "adamw_kernel"
         self.dominant_bytes = self.bytes_per_step
         self.description = (
-            "fused AdamW over one flat 1.2e9-element fp32 parameter (p, grad, exp_avg, exp_avg_sq), "
-            "lr 3e-4, betas (0.9, 0.95), eps 1e-8, wd 0.1; step = one optimizer step"
+            "fused AdamW over one flat 1.2e9-element fp32 parameter (p, grad, exp_avg, exp_avg_sq; the "
+            "moments in one allocation, as the fused optimizer creates them), lr 3e-4, betas (0.9, 0.95), "
+            "eps 1e-8, wd 0.1; step = one optimizer step"
         )
         self.lib = _lib.lib()
         self.stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -920,8 +921,8 @@ class AdamWListWorkload(Workload):
     """The fused AdamW step over a list of 100 fp32 parameters (1.2e9 elements in all), as a
     model's parameter list reaches torch.optim.AdamW (reference src/picotron/training/
     train_loop.py:308-325): the sizes of a decoder stack's projections (16.8M, 4.2M, 58.7M-class
-    matrices) with ten 4096-element norm weights among them, each tensor its own allocation, one
-    launch for all of them."""
+    matrices) with ten 4096-element norm weights among them, each parameter and gradient its own
+    allocation, the moments in one as the fused optimizer creates them, one launch for all."""
 
     name = "adamw_list"
     metric = "Fused AdamW step HBM GB/s & % of peak, 100 fp32 tensors, 1.2e9 params"
@@ -943,8 +944,10 @@ class AdamWListWorkload(Workload):
         self.n = sum(sizes)
         self.p = [_seeded((k,), torch.float32, 200 + i, 0.02) for i, k in enumerate(sizes)]
         self.g = [_seeded((k,), torch.float32, 400 + i, 1e-3) for i, k in enumerate(sizes)]
-        self.m = [torch.zeros(k, dtype=torch.float32, device="cuda") for k in sizes]
-        self.v = [torch.zeros(k, dtype=torch.float32, device="cuda") for k in sizes]
+        # the moments as the fused optimizer creates them (ops.adamw_moments: one allocation)
+        moments = ops.adamw_moments(self.p)
+        self.m = [m for m, _ in moments]
+        self.v = [v for _, v in moments]
         host, blocks = ops.adamw_table(self.p, self.g, self.m, self.v)
         self.table = host.cuda()
         self.blocks = blocks
@@ -955,7 +958,8 @@ class AdamWListWorkload(Workload):
         self.dominant_bytes = self.bytes_per_step
         self.description = (
             "fused AdamW over 100 fp32 parameters of decoder-projection sizes (1.2e9 elements, ten "
-            "4096-element norm weights among them), each its own allocation, lr 3e-4, betas (0.9, 0.95), "
+            "4096-element norm weights among them), each parameter and gradient its own allocation, the "
+            "moments in one (as the fused optimizer creates them), lr 3e-4, betas (0.9, 0.95), "
             "eps 1e-8, wd 0.1; step = one optimizer step (one launch)"
         )
         self.lib = _lib.lib()

@@ -177,9 +177,10 @@ def _plan(optimizer: Optimizer) -> tuple[list[tuple[dict, list[Tensor]]], torch.
 
 
 def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, list[Tensor]]:
-    """Host side of the fused step, touching no step counter: lazy state creation exactly as
+    """Host side of the fused step, touching no step counter: lazy state creation as
     torch.optim.Adam._init_group does for the non-fused case (a CPU fp32 step, or for a
-    capturable group an fp32 step on the parameter's device), and the record tables: one per
+    capturable group an fp32 step on the parameter's device; zeroed moments of the
+    parameter's shape, here views of one allocation per group), and the record tables: one per
     distinct next step value, or for a capturable group one with the table of its device
     steps.  Returns the launches and the parameters whose state was created here (so that a
     skipped step can remove it again)."""
@@ -192,6 +193,9 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
             continue
         beta1, beta2 = group["betas"]
         capturable = bool(group.get("capturable", False))
+        fresh = [p for p in params if len(state_of[p]) == 0]
+        # the group's new moments come from one allocation (ops.adamw_moments)
+        moments = iter(ops.adamw_moments(fresh))
         states = []
         for p in params:
             state = state_of[p]
@@ -200,8 +204,7 @@ def _prepare(optimizer: Optimizer, groups, device: torch.device) -> tuple[list, 
                     state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
                 else:
                     state["step"] = torch.tensor(0.0, dtype=torch.float32)
-                state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                state["exp_avg"], state["exp_avg_sq"] = next(moments)
                 created.append(p)
             states.append(state)
         hyper = dict(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],

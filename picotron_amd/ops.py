@@ -538,6 +538,30 @@ def adamw_table(
     return table, first
 
 
+_MOMENT_ALIGN = 64  # elements: every moment starts 256 bytes apart from the buffer's start
+
+
+def adamw_moments(params: list[Tensor]) -> list[tuple[Tensor, Tensor]]:
+    """Zeroed fp32 (exp_avg, exp_avg_sq) for each of ``params`` (one device, contiguous), as
+    views of one allocation: every first moment, then every second moment, each view with its
+    parameter's shape and 256-byte aligned.  The two moments of a parameter then lie a fixed
+    distance apart inside one allocation; as separate allocations their placement relative to
+    each other varies, and the update's four concurrent streams ran up to 8 % slower on some
+    placements (1.2e9 parameters: 5.70 against 5.40 ms per step on the same parameters and
+    gradients)."""
+
+    offsets = []
+    total = 0
+    for p in params:
+        offsets.append(total)
+        total += (p.numel() + _MOMENT_ALIGN - 1) // _MOMENT_ALIGN * _MOMENT_ALIGN
+    if not params:
+        return []
+    buf = torch.zeros(2 * total, dtype=torch.float32, device=params[0].device)
+    return [(buf[o:o + p.numel()].view(p.shape), buf[total + o:total + o + p.numel()].view(p.shape))
+            for p, o in zip(params, offsets)]
+
+
 def adamw_step(
     table_device: Tensor,
     total_blocks: int,
