@@ -245,6 +245,51 @@ def test_checkpoint_round_trip_continues_identically(gpu):
         close_fp32(sa["exp_avg_sq"], sb["exp_avg_sq"])
 
 
+def test_new_moments_share_one_allocation_and_save_like_torch(gpu):
+    """The fused step creates a group's moments as aligned, contiguous views of one allocation
+    (each with its parameter's shape); torch.save / torch.load of the state dict, as picotron's
+    checkpoint writes it (src/picotron/serialize/checkpoint.py:50), brings them back into a
+    torch optimizer that continues as the fused one does."""
+
+    import io
+
+    sizes = [(513, 7), (0,), (1000,), (1,), (64, 3)]
+    params = [torch.nn.Parameter(randn(sz, torch.float32, gpu, 50 + i, 0.02)) for i, sz in enumerate(sizes)]
+    opt = torch.optim.AdamW(params, **HP)
+    for p in params:
+        p.grad = randn(p.shape, torch.float32, gpu, 60 + p.numel(), 1e-3)
+    triton_adamw_step(opt)
+    moments = [opt.state[p][k] for p in params for k in ("exp_avg", "exp_avg_sq")]
+    base = moments[0].untyped_storage().data_ptr()
+    for p in params:
+        for k in ("exp_avg", "exp_avg_sq"):
+            m = opt.state[p][k]
+            assert m.shape == p.shape and m.is_contiguous() and m.dtype == torch.float32
+            assert m.untyped_storage().data_ptr() == base
+            assert m.numel() == 0 or m.data_ptr() % 256 == 0
+    # no two moments overlap
+    spans = sorted((m.data_ptr(), m.data_ptr() + 4 * m.numel()) for m in moments if m.numel())
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    buf.seek(0)
+    loaded = torch.load(buf, map_location=gpu, weights_only=True)
+    resumed = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    resumed_opt = torch.optim.AdamW(resumed, foreach=False, **HP)
+    resumed_opt.load_state_dict(loaded)
+    for a, b in zip(params, resumed):
+        a.grad = randn(a.shape, torch.float32, gpu, 70 + a.numel(), 1e-3)
+        b.grad = a.grad.clone()
+    triton_adamw_step(opt)
+    resumed_opt.step()
+    for a, b in zip(params, resumed):
+        close_fp32(a.detach(), b.detach())
+        close_fp32(opt.state[a]["exp_avg"], resumed_opt.state[b]["exp_avg"])
+        close_fp32(opt.state[a]["exp_avg_sq"], resumed_opt.state[b]["exp_avg_sq"])
+        assert float(opt.state[a]["step"]) == float(resumed_opt.state[b]["step"]) == 2.0
+
+
 def test_unaligned_views_and_missing_grads(gpu):
     flat = randn((10_001,), torch.float32, gpu, 9, 0.02)
     params = [torch.nn.Parameter(flat[1:5000].clone()), torch.nn.Parameter(flat[:7].clone())]
