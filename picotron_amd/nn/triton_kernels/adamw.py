@@ -27,6 +27,7 @@ applies it as it reads each gradient, instead of a separate read-modify-write pa
 
 from __future__ import annotations
 
+import threading
 import warnings
 
 import numpy as np
@@ -98,6 +99,7 @@ def _check_state(state: dict, p: Tensor, capturable: bool = False) -> None:
 
 _table_cache: dict[tuple, Tensor] = {}
 _TABLE_CACHE_SIZE = 16
+_table_lock = threading.Lock()  # optimizers may step from several threads at once
 # Tables used while a stream is being captured into a graph: the graph's kernels read them
 # on every replay, so they stay alive for the life of the process instead of leaving with
 # the cache's eviction.
@@ -112,19 +114,21 @@ def _device_table(host_table: Tensor, device: torch.device) -> Tensor:
     pinned host allocation and a host-to-device copy inside the graph."""
 
     key = (device, host_table.numpy().tobytes())
-    cached = _table_cache.pop(key, None)
     capturing = torch.cuda.is_current_stream_capturing()
+    with _table_lock:
+        cached = _table_cache.pop(key, None)
     if cached is None:
         if capturing:
             raise TritonAdamWUnavailable(
                 "HIP AdamW: the tensor table is first built during graph capture; run the "
                 "same call once before capturing it.")
         cached = host_table.pin_memory().to(device, non_blocking=True)
-    if capturing:
-        _captured_tables.append(cached)
-    _table_cache[key] = cached  # most recent last
-    while len(_table_cache) > _TABLE_CACHE_SIZE:
-        del _table_cache[next(iter(_table_cache))]
+    with _table_lock:
+        if capturing:
+            _captured_tables.append(cached)
+        _table_cache[key] = cached  # most recent last
+        while len(_table_cache) > _TABLE_CACHE_SIZE:
+            del _table_cache[next(iter(_table_cache))]
     return cached
 
 

@@ -119,3 +119,38 @@ def test_adamw_tables_skip_empty_tensors_in_one_order():
     assert table[:, 5].tolist() == [0, 1, 3]  # running sums of ceil(numel / block elements)
     assert blocks == 6
     assert step_table.tolist() == [steps[i].data_ptr() for i in kept]
+
+
+def test_last_error_is_per_thread():
+    """pt_last_error is the calling thread's message: a failure in one thread is not cleared
+    or overwritten by another thread's calls (the autograd engine issues backward calls from
+    its own device thread)."""
+
+    import threading
+
+    lib = _lib.lib()
+    first, second = threading.Barrier(2), threading.Barrier(2)
+    seen = {}
+
+    def failing():
+        seen["a_rc"] = lib.pt_swiglu_fwd(None, None, None, -1, 2, None)
+        first.wait()
+        second.wait()  # the other thread has failed differently and then succeeded
+        seen["a_msg"] = lib.pt_last_error().decode()
+
+    def other():
+        first.wait()
+        seen["b_fail"] = lib.pt_copy(None, None, 16, None)
+        seen["b_fail_msg"] = lib.pt_last_error().decode()
+        seen["b_ok"] = lib.pt_swiglu_fwd(None, None, None, 0, 2, None)
+        seen["b_msg"] = lib.pt_last_error().decode()
+        second.wait()
+
+    threads = [threading.Thread(target=failing), threading.Thread(target=other)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=30)
+    assert seen["a_rc"] == _lib.PT_EINVAL and seen["a_msg"].startswith("pt_swiglu_fwd")
+    assert seen["b_fail"] == _lib.PT_EINVAL and seen["b_fail_msg"].startswith("pt_copy")
+    assert seen["b_ok"] == _lib.PT_OK and seen["b_msg"] == ""
