@@ -82,3 +82,25 @@ def test_rope(gpu, reduce):
     REDUCTIONS[reduce](y_f).backward()
     REDUCTIONS[reduce](y_r).backward()
     close_fp32(xf.grad, xr.grad)
+
+
+def test_repeated_backward_with_retain_graph(gpu):
+    """RMSNorm (plain and with the residual add), SwiGLU and RoPE keep their saved tensors
+    intact through a backward: a second backward through the retained graph (as torch's own
+    ops allow) gives bit-identical gradients."""
+
+    x = randn((4, 40, 128), torch.float32, gpu, 20)
+    r = randn((4, 40, 128), torch.float32, gpu, 21)
+    w = randn((128,), torch.float32, gpu, 22, 0.1, 1.0)
+    g, u = randn((4, 40, 256), torch.float32, gpu, 23), randn((4, 40, 256), torch.float32, gpu, 24)
+    q = randn((2, 4, 40, 32), torch.float32, gpu, 25)
+    cos, sin = o_rope.tables(40, 32, 10_000.0, device=gpu)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (x, r, w, g, u, q)]
+    xl, rl, wl, gl, ul, ql = leaves
+    h, y = triton_residual_rms_norm(xl, rl, wl, 1e-6)
+    out = (triton_rms_norm(y, wl, 1e-6) * 0.5 + h).sum() + (triton_swiglu(gl, ul) ** 2).sum()
+    out = out + (triton_apply_rotary_embedding(ql, cos, sin) * 1.25).sum()
+    first = torch.autograd.grad(out, leaves, retain_graph=True)
+    second = torch.autograd.grad(out, leaves)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
