@@ -64,6 +64,26 @@ def _pytorch_backward(
 _backward_fallback_warned = False
 
 
+def _kernel_backward() -> bool:
+    """Whether a backward runs the HIP kernel.  A backward that builds a graph itself
+    (``create_graph=True``, for higher-order gradients) takes the reference's eager formula
+    instead (rmsnorm.py:110-134), which autograd can differentiate again as in the reference;
+    the kernel's gradient would enter that graph as a constant."""
+
+    return not torch.is_grad_enabled() or ops._compiling()
+
+
+def _warn_backward_fallback(error: Exception) -> None:
+    global _backward_fallback_warned
+    if not _backward_fallback_warned:
+        warnings.warn(
+            f"HIP RMSNorm backward unavailable; using PyTorch fallback: {error}",
+            RuntimeWarning,
+            stacklevel=3,
+        )
+        _backward_fallback_warned = True
+
+
 class _RMSNormAutogradFunction(torch.autograd.Function):
     """RMSNorm with a fused HIP forward and backward (or the PyTorch reference path)."""
 
@@ -91,23 +111,17 @@ class _RMSNormAutogradFunction(torch.autograd.Function):
         hidden_states, weight, saved_rms = ctx.saved_tensors
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if ctx.use_hip:
-            try:
-                grad_x, grad_w = ops.rmsnorm_bwd(
-                    grad_output, hidden_states, weight, saved_rms, need_dx=need_x, need_dw=need_w
-                )
-                return grad_x, grad_w, None, None
-            except _lib.HipKernelError as error:
-                # The reference backward cannot fail (it is eager PyTorch); keep that
-                # guarantee by recomputing with its formula.
-                global _backward_fallback_warned
-                if not _backward_fallback_warned:
-                    warnings.warn(
-                        f"HIP RMSNorm backward unavailable; using PyTorch fallback: {error}",
-                        RuntimeWarning,
-                        stacklevel=2,
+            if _kernel_backward():
+                try:
+                    grad_x, grad_w = ops.rmsnorm_bwd(
+                        grad_output, hidden_states, weight, saved_rms, need_dx=need_x, need_dw=need_w
                     )
-                    _backward_fallback_warned = True
-                saved_rms = saved_rms.unsqueeze(-1)
+                    return grad_x, grad_w, None, None
+                except _lib.HipKernelError as error:
+                    # The reference backward cannot fail (it is eager PyTorch); keep that
+                    # guarantee by recomputing with its formula.
+                    _warn_backward_fallback(error)
+            saved_rms = saved_rms.unsqueeze(-1)
         grad_x, grad_w = _pytorch_backward(hidden_states, weight, saved_rms, grad_output)
         return (grad_x if need_x else None), (grad_w if need_w else None), None, None
 
@@ -164,17 +178,13 @@ class _ResidualRMSNormFunction(torch.autograd.Function):
         if grad_y is None:
             grad = grad_h
         else:
-            try:
-                grad, grad_w = ops.residual_rmsnorm_bwd(grad_y, grad_h, h, weight, rstd, need_dw=need_w)
-            except _lib.HipKernelError as error:
-                global _backward_fallback_warned
-                if not _backward_fallback_warned:
-                    warnings.warn(
-                        f"HIP RMSNorm backward unavailable; using PyTorch fallback: {error}",
-                        RuntimeWarning,
-                        stacklevel=2,
-                    )
-                    _backward_fallback_warned = True
+            grad = None
+            if _kernel_backward():
+                try:
+                    grad, grad_w = ops.residual_rmsnorm_bwd(grad_y, grad_h, h, weight, rstd, need_dw=need_w)
+                except _lib.HipKernelError as error:
+                    _warn_backward_fallback(error)
+            if grad is None:
                 grad, grad_w = _pytorch_backward(h, weight, rstd.unsqueeze(-1), grad_y)
                 if grad_h is not None:
                     grad = (grad.float() + grad_h.float()).to(h.dtype)

@@ -24,33 +24,42 @@ class TritonRoPEUnavailable(RuntimeError):
 
 
 class _RoPEFunction(torch.autograd.Function):
-    """Rotate one or two (B, H, S, D) views by fp32 angle tables; backward = inverse."""
+    """Rotate one or two (B, H, S, D) views by fp32 angle tables (by minus the angles when
+    ``inverse``); the backward is the rotation the other way."""
 
     @staticmethod
-    def forward(ctx, layout: str, cosine: Tensor, sine: Tensor, *states: Tensor):  # type: ignore[override]
+    def forward(ctx, layout: str, inverse: bool, cosine: Tensor, sine: Tensor, *states: Tensor):  # type: ignore[override]
         ctx.layout = layout
+        ctx.inverse = inverse
         ctx.save_for_backward(cosine, sine)
         ctx.count = len(states)
         out0, out1 = ops.rope(
-            states[0], cosine, sine, layout=layout, x1=states[1] if len(states) > 1 else None
+            states[0], cosine, sine, layout=layout, inverse=inverse,
+            x1=states[1] if len(states) > 1 else None,
         )
         return (out0,) if out1 is None else (out0, out1)
 
     @staticmethod
     def backward(ctx, *grads: Tensor):  # type: ignore[override]
         cosine, sine = ctx.saved_tensors
-        present = [i for i, g in enumerate(grads) if g is not None and ctx.needs_input_grad[3 + i]]
+        present = [i for i, g in enumerate(grads) if g is not None and ctx.needs_input_grad[4 + i]]
         results: list[Tensor | None] = [None] * ctx.count
         if present:
             g = [_last_dim_contiguous(grads[i]) for i in present]
-            d0, d1 = ops.rope(
-                g[0], cosine, sine, layout=ctx.layout, inverse=True,
-                x1=g[1] if len(g) > 1 else None,
-            )
+            if torch.is_grad_enabled() and not ops._compiling():
+                # create_graph=True: the backward rotation as this Function again, so that
+                # autograd can differentiate it to any order
+                d = _RoPEFunction.apply(ctx.layout, not ctx.inverse, cosine, sine, *g)
+                d0, d1 = d[0], (d[1] if len(d) > 1 else None)
+            else:
+                d0, d1 = ops.rope(
+                    g[0], cosine, sine, layout=ctx.layout, inverse=not ctx.inverse,
+                    x1=g[1] if len(g) > 1 else None,
+                )
             results[present[0]] = d0
             if len(present) > 1:
                 results[present[1]] = d1
-        return (None, None, None, *results)
+        return (None, None, None, None, *results)
 
 
 def _last_dim_contiguous(t: Tensor) -> Tensor:
@@ -95,7 +104,7 @@ def triton_apply_rotary_embedding(
     """
 
     _validate([states], cosine, sine)
-    return _RoPEFunction.apply(layout, cosine.float(), sine.float(), states)[0]
+    return _RoPEFunction.apply(layout, False, cosine.float(), sine.float(), states)[0]
 
 
 def triton_apply_rotary_embedding_pair(
@@ -104,5 +113,5 @@ def triton_apply_rotary_embedding_pair(
     """Rotate query and key (GQA: head counts may differ) in one kernel launch."""
 
     _validate([query, key], cosine, sine)
-    out_q, out_k = _RoPEFunction.apply(layout, cosine.float(), sine.float(), query, key)
+    out_q, out_k = _RoPEFunction.apply(layout, False, cosine.float(), sine.float(), query, key)
     return out_q, out_k

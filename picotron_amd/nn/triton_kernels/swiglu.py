@@ -43,7 +43,9 @@ class _SwiGLUAutogradFunction(torch.autograd.Function):
         ctx: torch.autograd.function.FunctionCtx, grad_output: Tensor
     ) -> tuple[Tensor | None, Tensor | None, None]:
         gate, up = ctx.saved_tensors
-        if ctx.use_hip:
+        # A backward that builds a graph itself (create_graph=True) takes the reference's
+        # eager formula below, which autograd can differentiate again.
+        if ctx.use_hip and (not torch.is_grad_enabled() or ops._compiling()):
             grad_gate, grad_up = ops.swiglu_bwd(
                 grad_output, gate, up, ctx.needs_input_grad[0], ctx.needs_input_grad[1]
             )

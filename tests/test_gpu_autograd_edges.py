@@ -104,3 +104,65 @@ def test_repeated_backward_with_retain_graph(gpu):
     second = torch.autograd.grad(out, leaves)
     for a, b in zip(first, second):
         assert torch.equal(a, b)
+
+
+def _first_and_second(fn, inputs, v, weights):
+    """First-order gradients of (fn(*inputs) * v).sum() with create_graph=True, then the
+    gradient of sum(g_i * weights_i) with respect to the inputs and v."""
+
+    leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+    vl = v.detach().clone().requires_grad_(True)
+    out = fn(*leaves)
+    outs = out if isinstance(out, tuple) else (out,)
+    total = sum((o * vl).sum() for o in outs)
+    first = torch.autograd.grad(total, leaves, create_graph=True)
+    z = sum((g * a).sum() for g, a in zip(first, weights))
+    second = torch.autograd.grad(z, leaves + [vl], allow_unused=True)
+    return [g.detach() for g in first], second
+
+
+def _close_all(a_list, b_list):
+    for a, b in zip(a_list, b_list):
+        if a is None or b is None:
+            assert a is None and b is None or float((a if a is not None else b).abs().max()) == 0.0
+            continue
+        close_fp32(a, b, scale=float(b.abs().max()) * 10 + 1e-30)
+
+
+@pytest.mark.parametrize("op", ["rmsnorm", "residual_rmsnorm", "swiglu", "rope"])
+def test_higher_order_gradients_follow_the_reference_formulas(gpu, op):
+    """With create_graph=True the fused ops' backwards build a graph as the reference's eager
+    backwards do (rmsnorm.py:110-134, swiglu.py:71-81; RoPE's backward is a rotation), so
+    second-order gradients equal the reference path's instead of treating the kernel's
+    gradient as a constant."""
+
+    if op == "rmsnorm":
+        x, w = randn((3, 17, 96), torch.float32, gpu, 30), randn((96,), torch.float32, gpu, 31, 0.1, 1.0)
+        inputs, v = [x, w], randn((3, 17, 96), torch.float32, gpu, 32)
+        fused = lambda a, b: triton_rms_norm(a, b, 1e-6)  # noqa: E731
+        ref = lambda a, b: rms_norm_with_pytorch_forward(a, b, 1e-6)  # noqa: E731
+    elif op == "residual_rmsnorm":
+        x, r = randn((3, 17, 96), torch.float32, gpu, 33), randn((3, 17, 96), torch.float32, gpu, 34)
+        w = randn((96,), torch.float32, gpu, 35, 0.1, 1.0)
+        inputs, v = [x, r, w], randn((3, 17, 96), torch.float32, gpu, 36)
+        fused = lambda a, b, c: triton_residual_rms_norm(a, b, c, 1e-6)  # noqa: E731
+
+        def ref(a, b, c):
+            h = a + b
+            return h, rms_norm_with_pytorch_forward(h, c, 1e-6)
+    elif op == "swiglu":
+        inputs = [randn((5, 70), torch.float32, gpu, 37), randn((5, 70), torch.float32, gpu, 38)]
+        v = randn((5, 70), torch.float32, gpu, 39)
+        fused, ref = triton_swiglu, swiglu_with_pytorch_forward
+    else:
+        inputs, v = [randn((2, 3, 19, 32), torch.float32, gpu, 40)], randn((2, 3, 19, 32), torch.float32, gpu, 41)
+        cos, sin = o_rope.tables(19, 32, 10_000.0, device=gpu)
+        fused = lambda a: triton_apply_rotary_embedding(a, cos, sin)  # noqa: E731
+        ref = lambda a: apply_rotary_embedding(a, cos, sin)  # noqa: E731
+    weights = [randn(t.shape, torch.float32, gpu, 50 + i) for i, t in enumerate(inputs)]
+    first_f, second_f = _first_and_second(fused, inputs, v, weights)
+    first_r, second_r = _first_and_second(ref, inputs, v, weights)
+    _close_all(first_f, first_r)
+    _close_all(second_f, second_r)
+    # the second-order gradient reaches the upstream gradient v in every op
+    assert second_f[-1] is not None and float(second_f[-1].abs().max()) > 0
