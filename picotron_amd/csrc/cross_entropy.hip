@@ -204,10 +204,7 @@ __device__ __forceinline__ RowRef row_ref(int64_t row, int64_t inner, int64_t va
 // past the end (they return 0) and stores past the end, so a row's ragged last vectors need
 // no branches.  The range check covers the VGPR offset plus the instruction's immediate offset
 // but not the SGPR offset, so every access below puts its whole offset in the VGPR operand
-// and passes an SGPR offset of 0.  kBufferWord3 is the gfx9-family data-format word for
-// untyped 32-bit access.
-constexpr int kBufferWord3 = 0x00020000;
-constexpr int kNonTemporal = 2;  // buffer cache policy bit: no reuse expected
+// and passes an SGPR offset of 0 (kBufferWord3 and the cache-policy bits: pt_common.hpp).
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kBufferWord3);

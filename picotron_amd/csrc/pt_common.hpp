@@ -97,6 +97,31 @@ union Vec16 {
   T e[16 / sizeof(T)];
 };
 
+// ------------------------------------------------------------------ buffer resources
+
+// Data-format word of a raw (untyped, 32-bit) gfx9-family buffer resource.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of buffer loads and stores on gfx950: bit 0 sc0, bit 1 nt, bit 4 sc1.
+constexpr int kNonTemporal = 2;  // nt: no reuse expected
+// nt | sc1: a store performed at device scope, written through the XCD's L2 rather than
+// left dirty there for the write-back at the end of the kernel.  A 134 MB copy on MI355X
+// (one 16-byte vector per thread, nontemporal loads, one-shot grid) takes 43.2-43.4 us per
+// launch with these stores, 44.4-44.7 us with nontemporal write-back stores and 47.1 us with
+// plain ones.
+constexpr int kWriteThrough = 18;
+
+// A raw buffer resource over `bytes` bytes at `base`, which must be the same in every active
+// lane of the wave: it is read from the first active lane, so the resource lives in scalar
+// registers and addresses are per-lane byte offsets from it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_buffer(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32)));
+  void* b = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(b, 0, bytes, kBufferWord3);
+}
+
 // Loads 16 bytes from `p` (16-byte aligned).  NT selects a nontemporal access, used
 // for data that is touched exactly once (streams far larger than L2 + MALL).
 template <bool NT>

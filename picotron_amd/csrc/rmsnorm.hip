@@ -11,35 +11,16 @@ namespace rmsnorm {
 __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
                                                                 int64_t nparts, int cols,
                                                                 void* __restrict__ dw, int wdt) {
-  constexpr int kGroups = 256 / kFinishCols;
-  constexpr int kUnroll = 64;
-  __shared__ float lds[kGroups][kFinishCols + 1];
+  __shared__ float lds[kFinishGroups][kFinishCols + 1];
   const int col = threadIdx.x % kFinishCols;
   const int grp = threadIdx.x / kFinishCols;
   const int c = blockIdx.x * kFinishCols + col;
-  float s = 0.0f;
-  if (c < cols) {
-    const float* p = partial + c;
-    int64_t i = grp;
-    for (; i + static_cast<int64_t>(kGroups) * (kUnroll - 1) < nparts;
-         i += static_cast<int64_t>(kGroups) * kUnroll) {
-      float v[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) v[u] = p[(i + u * kGroups) * cols];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) s += v[u];
-    }
-    // The remainder (fewer than kUnroll partials per group) in batches of 16 independent
-    // loads, so that it costs a few round trips rather than one per partial.
-#pragma unroll 16
-    for (; i < nparts; i += kGroups) s += p[i * cols];
-  }
-  lds[grp][col] = s;
+  lds[grp][col] = c < cols ? column_group_sum(partial, nparts, cols, c, grp) : 0.0f;
   __syncthreads();
   if (grp == 0 && c < cols) {
     float t = lds[0][col];
 #pragma unroll
-    for (int g = 1; g < kGroups; ++g) t += lds[g][col];
+    for (int g = 1; g < kFinishGroups; ++g) t += lds[g][col];
     store_any(dw, c, wdt, t);
   }
 }
@@ -81,17 +62,16 @@ namespace {
 int fwd_impl(const char* fn, const void* x, int64_t xs, const void* res, int64_t res_s,
              const void* weight, void* h, int64_t hs, void* y, int64_t ys, float* rstd,
              int64_t rows, int64_t cols, float eps, int x_dtype, int w_dtype, void* stream) {
-  const std::string name(fn);
   Shape s;
   if (int rc = validate(fn, rows, cols, x_dtype, w_dtype, false, &s)) return rc;
   if (rows == 0) return ok();
   const bool fused = res != nullptr || h != nullptr;
   if (!x || !weight || !y || !rstd || (fused && (!res || !h)))
-    return fail(PT_EINVAL, name + ": null pointer");
+    return fail(PT_EINVAL, std::string(fn) + ": null pointer");
   if (rows > 1 && (xs < cols || ys < cols || (fused && (res_s < cols || hs < cols))))
-    return fail(PT_EINVAL, name + ": row stride smaller than cols");
+    return fail(PT_EINVAL, std::string(fn) + ": row stride smaller than cols");
   if (fused && (h == x || h == res || h == y))
-    return fail(PT_EINVAL, name + ": h must not alias x, residual or y");
+    return fail(PT_EINVAL, std::string(fn) + ": h must not alias x, residual or y");
   const int vec = 16 / dtype_size(x_dtype);
   FwdArgs a{};
   a.x = x;
@@ -123,7 +103,7 @@ int fwd_impl(const char* fn, const void* x, int64_t xs, const void* res, int64_t
   } else {
     launched = launch_fwd<__bf16>(a);
   }
-  if (!launched) return fail(PT_EUNSUPPORTED, name + ": no kernel for this shape");
+  if (!launched) return fail(PT_EUNSUPPORTED, std::string(fn) + ": no kernel for this shape");
   return check_launch(fn);
 }
 
@@ -131,7 +111,6 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
              const void* x, int64_t xs, const void* weight, const float* rstd, void* dx,
              int64_t dxs, void* dweight, void* workspace, size_t workspace_bytes, int64_t rows,
              int64_t cols, int x_dtype, int w_dtype, void* stream, bool static_scratch = false) {
-  const std::string name(fn);
   Shape s;
   if (int rc = validate(fn, rows, cols, x_dtype, w_dtype, true, &s)) return rc;
   hipStream_t st = as_stream(stream);
@@ -141,9 +120,9 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
     return ok();
   }
   if (!dy || !x || !weight || !rstd || (dh_in && !dx))
-    return fail(PT_EINVAL, name + ": null pointer");
+    return fail(PT_EINVAL, std::string(fn) + ": null pointer");
   if (rows > 1 && (dys < cols || xs < cols || (dx && dxs < cols) || (dh_in && dh_in_s < cols)))
-    return fail(PT_EINVAL, name + ": row stride smaller than cols");
+    return fail(PT_EINVAL, std::string(fn) + ": row stride smaller than cols");
   const int vec = 16 / dtype_size(x_dtype);
   BwdArgs a{};
   a.aligned = (cols % vec == 0) && rows_aligned(x_dtype, dy, dys) &&
@@ -157,15 +136,15 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
     const size_t need = static_cast<size_t>(a.blocks) * static_cast<size_t>(cols) * sizeof(float);
     if (static_scratch && need > workspace_bytes)
       return fail(PT_EUNSUPPORTED,
-                  name + ": the weight-gradient partials need " + std::to_string(need) +
+                  std::string(fn) + ": the weight-gradient partials need " + std::to_string(need) +
                       " bytes, more than the library's static scratch of " +
                       std::to_string(workspace_bytes) + " bytes; use pt_rmsnorm_bwd");
     if (!workspace || workspace_bytes < need)
-      return fail(PT_EINVAL, name + ": workspace smaller than pt_rmsnorm_bwd_workspace_bytes()");
-    if (!aligned16(workspace)) return fail(PT_EINVAL, name + ": workspace not aligned");
+      return fail(PT_EINVAL, std::string(fn) + ": workspace smaller than pt_rmsnorm_bwd_workspace_bytes()");
+    if (!aligned16(workspace)) return fail(PT_EINVAL, std::string(fn) + ": workspace not aligned");
     // LDS combining the row slots' weight-gradient sums holds one fp32 per column.
     if (bwd_waves(a.shape) / a.shape.wpr > 1 && cols * 4 > 160 * 1024)
-      return fail(PT_EUNSUPPORTED, name + ": hidden size too large for the LDS combine");
+      return fail(PT_EUNSUPPORTED, std::string(fn) + ": hidden size too large for the LDS combine");
     partial = static_cast<float*>(workspace);
   }
   a.dy = dy;
@@ -192,7 +171,7 @@ int bwd_impl(const char* fn, const void* dy, int64_t dys, const void* dh_in, int
   } else {
     launched = launch_bwd<__bf16>(a);
   }
-  if (!launched) return fail(PT_EUNSUPPORTED, name + ": no kernel for this shape");
+  if (!launched) return fail(PT_EUNSUPPORTED, std::string(fn) + ": no kernel for this shape");
   if (int rc = check_launch(fn)) return rc;
   if (dweight) {
     const unsigned fblocks = static_cast<unsigned>((cols + kFinishCols - 1) / kFinishCols);
@@ -221,22 +200,35 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 namespace {
 
 constexpr int kScratchDevices = 64;
-std::once_flag g_scratch_once[kScratchDevices];
+std::mutex g_scratch_mu;
+bool g_scratch_looked_up[kScratchDevices];
 void* g_scratch_ptr[kScratchDevices];
 hipError_t g_scratch_err[kScratchDevices];
 
 // Device address of the current device's copy of `scratch`, looked up once per device with
 // that device current.  In host code the array's name is only a host-side stand-in for the
-// symbol: kernels and copies must be given this address instead.
-int scratch_address(const char* fn, void** out) {
+// symbol: kernels and copies must be given this address instead.  The lookup is kept out of
+// graph captures (it may load the library's code on the device): the first call on a device
+// must not be captured, and is refused if it is.
+int scratch_address(const char* fn, hipStream_t st, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
     return fail(PT_EDEVICE, std::string(fn) + ": no current HIP device");
-  std::call_once(g_scratch_once[dev], [dev] {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_looked_up[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+      (void)hipGetLastError();
+      return fail(PT_EUNSUPPORTED, std::string(fn) +
+                                       ": the first call on a device looks up the library's "
+                                       "scratch and cannot be captured; call it once before "
+                                       "capturing");
+    }
     void* p = nullptr;
     g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
-  });
+    g_scratch_looked_up[dev] = true;
+  }
   if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
     return fail(PT_EDEVICE, std::string(fn) + ": hipGetSymbolAddress(scratch) failed: " +
                                 hipGetErrorString(g_scratch_err[dev]));
@@ -289,7 +281,7 @@ int pt_rmsnorm_bwd_noalloc(const void* dy, int64_t dy_row_stride, const void* x,
   static const char* const fn = "pt_rmsnorm_bwd_noalloc";
   void* ws = nullptr;
   if (dweight != nullptr && rows > 0) {
-    if (int rc = scratch_address(fn, &ws)) return rc;
+    if (int rc = scratch_address(fn, as_stream(stream), &ws)) return rc;
   }
   return bwd_impl(fn, dy, dy_row_stride, nullptr, 0, x, x_row_stride, weight, rstd, dx,
                   dx_row_stride, dweight, ws, ws ? kScratchBytes : 0, rows, cols, x_dtype, w_dtype,

@@ -34,10 +34,9 @@ namespace rmsnorm {
 // forward 4, or in both cases as many as a row spans when that is more.
 constexpr int kBwdWaves = 8;
 constexpr int kFwdWaves = 4;
-// Cache policy of the row streams (x, dy loads; y, dx stores): nontemporal accesses are
-// the measured optimum on MI355X for data read or written once per kernel.
+// Cache policy of the row loads (x, dy): nontemporal, the measured optimum on MI355X for data
+// read once per kernel.  The row stores: RowStore.
 constexpr bool kLoadNT = true;
-constexpr bool kStoreNT = true;
 // Rows the backward keeps in flight ahead of the one it is reducing (0, 1 or 2).
 constexpr int kBwdPrefetch = 1;
 
@@ -198,20 +197,42 @@ __device__ __forceinline__ void load_row(const T* __restrict__ row, int rl, int 
   }
 }
 
-template <typename T, int LANES, bool ALIGNED, bool NT>
-__device__ __forceinline__ void store_vec(T* __restrict__ row, int rl, int k, int cols,
-                                          const float (&o)[Elem<T>::VEC]) {
-  constexpr int V = Elem<T>::VEC;
-  const int e = (rl + k * LANES) * V;
-  const int valid = cols - e;
-  if (valid > 0) store_f32<T, ALIGNED, NT>(row + e, o, valid);
-}
-
 // True if vector k of lane rl lies inside the row (aligned path: whole vectors).
 template <typename T, int LANES>
 __device__ __forceinline__ bool in_row(int rl, int k, int cols) {
   return (rl + k * LANES) * Elem<T>::VEC < cols;
 }
+
+// Stores of one row's 16-byte vectors.  Aligned rows: buffer stores with cache policy
+// POLICY through a resource over the row, whose base is wave-uniform (all lanes of a wave
+// work on the same row); the resource's range check drops vectors past the row end, so the
+// stores need no branch.  Unaligned rows: element stores of the in-range elements.
+// The forward's stores are write-through (kWriteThrough: 43.9 against 44.3 us per launch at
+// [16384, 4096] bf16), the backward's nontemporal (kNonTemporal: 71.9 against 72.2 us: with
+// two read streams beside it, write-through costs more than it saves).
+template <typename T, int LANES, bool ALIGNED, int POLICY>
+struct RowStore {
+  T* row;
+  int cols;
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ __forceinline__ RowStore(T* r, int c) : row(r), cols(c) {
+    if constexpr (ALIGNED) rsrc = uniform_buffer(r, c * static_cast<int>(sizeof(T)));
+  }
+  __device__ __forceinline__ void store(int rl, int k, const float (&o)[Elem<T>::VEC]) const {
+    constexpr int V = Elem<T>::VEC;
+    const int e = (rl + k * LANES) * V;
+    if constexpr (ALIGNED) {
+      Vec16<T> v;
+#pragma unroll
+      for (int i = 0; i < V; ++i) v.e[i] = Elem<T>::from_f32(o[i]);
+      __builtin_amdgcn_raw_buffer_store_b128(v.raw, rsrc, e * static_cast<int>(sizeof(T)), 0,
+                                             POLICY);
+    } else {
+      const int valid = cols - e;
+      if (valid > 0) store_f32<T, false>(row + e, o, valid);
+    }
+  }
+};
 
 // Sum over the WPR waves that share a row.  `red` holds 2*WAVES floats; `buf` alternates
 // between consecutive calls so one barrier per row suffices (a wave cannot overwrite a
@@ -248,7 +269,7 @@ __device__ __forceinline__ float row_sum(float v, float* red, int wave, int lane
 // stored sum.
 
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT, bool PERSIST, bool ADD>
+          bool PERSIST, bool ADD>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     const T* __restrict__ x, int64_t xs, const void* __restrict__ w, int wdt, T* __restrict__ y,
     int64_t ys, float* __restrict__ rstd, int64_t rows, int cols, float eps, int iters,
@@ -280,7 +301,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     RowRegs<T, VPL>& xr = rw.x;
     const bool active = row < r1;
     if constexpr (ADD) {
-      T* hr = rin.h + row * rin.h_stride;
+      const RowStore<T, LANES, ALIGNED, kWriteThrough> hs(rin.h + row * rin.h_stride, cols);
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         float o[V];
@@ -289,7 +310,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
           xr.v[k].e[i] = Elem<T>::from_f32(xr.at(k, i) + rw.res.at(k, i));
           o[i] = xr.at(k, i);
         }
-        if (active) store_vec<T, LANES, ALIGNED, STORE_NT>(hr, rl, k, cols, o);
+        if (active) hs.store(rl, k, o);
       }
     }
     float ss = 0.0f;
@@ -310,13 +331,13 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
     if (!active) return;
     const float r = 1.0f / sqrtf(ss * inv_cols + eps);
     if (rl == 0) rstd[row] = r;
-    T* yr = y + row * ys;
+    const RowStore<T, LANES, ALIGNED, kWriteThrough> yst(y + row * ys, cols);
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
       float o[V];
 #pragma unroll
       for (int i = 0; i < V; ++i) o[i] = (xr.at(k, i) * r) * wv.at(k, i);
-      store_vec<T, LANES, ALIGNED, STORE_NT>(yr, rl, k, cols, o);
+      yst.store(rl, k, o);
     }
   };
 
@@ -359,6 +380,40 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
   }
 }
 
+// ------------------------------------------------------------------ weight-gradient sum
+//
+// dW[c] = sum_p partial[p][c] in a fixed order, cast to the weight type: 256 threads cover
+// kFinishCols columns with kFinishGroups groups of 32 lanes; group g sums p = g, g+8, ... in
+// increasing p (up to 64 loads in flight per lane: one round trip at 512 partials), then the
+// groups are added in group order (rmsnorm_dw_finish_kernel).
+constexpr int kFinishCols = 32;
+constexpr int kFinishGroups = 8;
+
+__device__ __forceinline__ float column_group_sum(const float* __restrict__ partial,
+                                                  int64_t nparts, int cols, int c, int grp) {
+  constexpr int kUnroll = 64;
+  const float* p = partial + c;
+  float s = 0.0f;
+  int64_t i = grp;
+  for (; i + static_cast<int64_t>(kFinishGroups) * (kUnroll - 1) < nparts;
+       i += static_cast<int64_t>(kFinishGroups) * kUnroll) {
+    float v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) v[u] = p[(i + u * kFinishGroups) * cols];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) s += v[u];
+  }
+  // The remainder (fewer than kUnroll partials per group) in batches of 16 independent
+  // loads, so that it costs a few round trips rather than one per partial.
+#pragma unroll 16
+  for (; i < nparts; i += kFinishGroups) s += p[i * cols];
+  return s;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
+                                                                int64_t nparts, int cols,
+                                                                void* __restrict__ dw, int wdt);
+
 // ------------------------------------------------------------------ backward
 //
 // Persistent blocks walking the same interleaved row groups as the forward (step `it`:
@@ -375,7 +430,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_fwd_kernel(
 // same lane).
 
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool STORE_NT, bool ADD, int PREFETCH = kBwdPrefetch>
+          bool ADD, int PREFETCH = kBwdPrefetch>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, int64_t dys, const T* __restrict__ x, int64_t xs,
     const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* dx,
@@ -443,7 +498,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const float dm = dot * inv_cols;
     const float r2 = r * r;
     if (dx != nullptr) {
-      T* dxr = dx + row * dxs;
+      const RowStore<T, LANES, ALIGNED, kNonTemporal> dxst(dx + row * dxs, cols);
 #pragma unroll
       for (int k = 0; k < VPL; ++k) {
         float o[V];
@@ -452,7 +507,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
           o[i] = r * (bf.g.at(k, i) * wv[k][i] - (bf.x.at(k, i) * r2) * dm);
           if constexpr (ADD) o[i] += bf.d.at(k, i);
         }
-        store_vec<T, LANES, ALIGNED, STORE_NT>(dxr, rl, k, cols, o);
+        dxst.store(rl, k, o);
       }
     }
     if (want_dw) {
@@ -552,15 +607,6 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
   }
 }
 
-// dW[c] = sum_p partial[p][c] in a fixed order, cast to the weight type.  A block covers
-// kFinishCols columns with 8 groups of 32 lanes; group g sums p = g, g+8, ... in increasing
-// p (up to 64 loads in flight per lane: one round trip at 512 partials), then the groups
-// are added in group order.
-constexpr int kFinishCols = 32;
-__global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __restrict__ partial,
-                                                                int64_t nparts, int cols,
-                                                                void* __restrict__ dw, int wdt);
-
 // ------------------------------------------------------------------ host-side shapes
 
 struct Shape {
@@ -570,7 +616,8 @@ struct Shape {
 
 // Launch tuning.  Defaults were chosen by measurement on MI355X; the environment can
 // override them (PT_RMSNORM_FWD_VPL_CAP, PT_RMSNORM_BWD_VPL_CAP, PT_RMSNORM_FWD_BLOCKS_PER_CU,
-// PT_RMSNORM_BWD_PARTIALS), read once per process.  The backward partial count fixes the
+// PT_RMSNORM_BWD_PARTIALS, PT_RMSNORM_FWD_OCCUPANCY, PT_RMSNORM_BWD_OCCUPANCY), read once
+// per process.  The backward partial count fixes the
 // weight-gradient summation order, so dW is reproducible for a given setting.
 struct Tuning {
   int fwd_vpl_cap = 4;
@@ -751,7 +798,7 @@ struct FwdLaunch {
     constexpr int WAVES = WPR > kFwdWaves ? WPR : kFwdWaves;
     const ResidualIn<T> rin{static_cast<const T*>(a.res), a.res_s, static_cast<T*>(a.h), a.h_s};
     const auto kernel =
-        rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, PERSIST, ADD>;
+        rmsnorm_fwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, PERSIST, ADD>;
     size_t lds = occupancy_lds(tuning().fwd_occupancy, 0);
     if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
@@ -779,6 +826,16 @@ struct FwdLaunch {
 template <typename T, typename WT, bool ALIGNED>
 struct BwdLaunch {
   const BwdArgs& a;
+  template <bool ADD, int VPL, int WPR, int WAVES>
+  void go(size_t need, size_t lds, int iters) const {
+    const auto kernel = rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, ADD>;
+    if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = need;
+    const ResidualGrad<T> rg{static_cast<const T*>(a.dh_in), a.dh_in_s};
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds, a.st,
+                       static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x), a.xs, a.w,
+                       a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows, a.cols,
+                       iters, rg);
+  }
   template <int VPL, int WPR>
   void run() const {
     constexpr int WAVES = WPR > kBwdWaves ? WPR : kBwdWaves;
@@ -786,23 +843,12 @@ struct BwdLaunch {
     const size_t need =
         (RPB > 1 && a.partial != nullptr) ? static_cast<size_t>(a.cols) * sizeof(float) : 0;
     const size_t share = occupancy_lds(tuning().bwd_occupancy, 0);
-    size_t lds = share > need ? share : need;
-    const ResidualGrad<T> rg{static_cast<const T*>(a.dh_in), a.dh_in_s};
+    const size_t lds = share > need ? share : need;
     const int iters = row_iters(a.rows, a.blocks, RPB);
     if (a.dh_in != nullptr) {
-      const auto kernel = rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, true>;
-      if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = need;
-      hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds,
-                         a.st, static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x),
-                         a.xs, a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
-                         a.cols, iters, rg);
+      go<true, VPL, WPR, WAVES>(need, lds, iters);
     } else {
-      const auto kernel = rmsnorm_bwd_kernel<T, WT, VPL, WPR, WAVES, ALIGNED, kLoadNT, kStoreNT, false>;
-      if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = need;
-      hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.blocks)), dim3(WAVES * 64), lds,
-                         a.st, static_cast<const T*>(a.dy), a.dys, static_cast<const T*>(a.x),
-                         a.xs, a.w, a.wdt, a.rstd, static_cast<T*>(a.dx), a.dxs, a.partial, a.rows,
-                         a.cols, iters, rg);
+      go<false, VPL, WPR, WAVES>(need, lds, iters);
     }
   }
 };

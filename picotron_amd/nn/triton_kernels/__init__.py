@@ -7,6 +7,7 @@ src/picotron/nn/triton_kernels/__init__.py:1-41); each fast path raises its
 
 from picotron_amd.nn.triton_kernels.adamw import (
     AdamWStepWithFallback,
+    FusedAdamWStepFailed,
     TritonAdamWUnavailable,
     triton_adamw_step,
     triton_clip_grad_norm_and_step,
@@ -58,6 +59,7 @@ __all__ = [
     "swiglu_with_pytorch_forward",
     "rms_norm_with_pytorch_forward",
     # additions beyond the reference surface
+    "FusedAdamWStepFailed",
     "triton_adamw_step",
     "triton_apply_rotary_embedding_pair",
     "triton_clip_grad_norm_and_step",

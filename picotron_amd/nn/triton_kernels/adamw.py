@@ -42,6 +42,25 @@ class TritonAdamWUnavailable(RuntimeError):
     """Raised when the fused (HIP) AdamW step cannot run for this optimizer."""
 
 
+class FusedAdamWStepFailed(RuntimeError):
+    """The fused step failed after it had begun to change the optimizer's state or the
+    gradients (step counters advanced, a gradient unscaled, an update launched).  Running
+    torch's step after it would apply part of the update twice, so the fallbacks of
+    :class:`AdamWStepWithFallback` let this error through instead of retrying."""
+
+
+def _committed(fn, *args, **kwargs):
+    """Runs the state-changing part of a fused step: any error becomes FusedAdamWStepFailed."""
+
+    try:
+        return fn(*args, **kwargs)
+    except FusedAdamWStepFailed:
+        raise
+    except Exception as error:
+        raise FusedAdamWStepFailed(
+            f"the fused AdamW step failed after changing optimizer state: {error}") from error
+
+
 def _reject(reason: str) -> TritonAdamWUnavailable:
     return TritonAdamWUnavailable(f"Fused HIP AdamW is not implemented for {reason}; using PyTorch AdamW instead.")
 
@@ -251,8 +270,14 @@ def _next_step(value: float) -> float:
 def _launch(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | None,
             write_grad: bool) -> None:
     """Advances every stepped parameter's step counter (as torch's AdamW does: on the host,
-    or for a capturable group on the device) and launches the prepared updates."""
+    or for a capturable group on the device) and launches the prepared updates.  It changes
+    state from its first line, so any error in it is FusedAdamWStepFailed."""
 
+    _committed(_launch_all, optimizer, groups, launches, grad_scale, write_grad)
+
+
+def _launch_all(optimizer: Optimizer, groups, launches: list, grad_scale: Tensor | None,
+                write_grad: bool) -> None:
     state_of = optimizer.state
     for group, params in groups:
         if params:
@@ -473,7 +498,16 @@ def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float |
         raise _reject("a loss scale on another device than the gradients")
     grads = [p.grad for _, params in groups for p in params]
     table, blocks = _grad_table(grads, device)
-    # every check that can fail is done: from here on the call runs to the end
+    # every check that can fail is done: from here on the call runs to the end, and an error
+    # (a failed launch) is FusedAdamWStepFailed, never a reason to run torch's sequence again
+    return _committed(_grad_scaler_step_committed, grad_scaler, state, optimizer, groups,
+                      device, scale, table, blocks, max_norm)
+
+
+def _grad_scaler_step_committed(grad_scaler, state, optimizer, groups, device, scale, table,
+                                blocks, max_norm) -> bool:
+    from torch.amp.grad_scaler import OptState
+
     inv_scale = scale.double().reciprocal().float()
     _, multiplier, found_inf = ops.grad_stats(
         table, blocks, inv_scale, max_norm, ops.CLIP_CLAMP)
@@ -501,7 +535,9 @@ class AdamWStepWithFallback:
 
     def step(self, optimizer: Optimizer, max_grad_norm: float | None = None) -> None:
         """``optimizer.step()``; with ``max_grad_norm`` the gradients are first clipped as
-        ``torch.nn.utils.clip_grad_norm_`` does (fused into the step on the fast path)."""
+        ``torch.nn.utils.clip_grad_norm_`` does (fused into the step on the fast path).  An
+        error raised after the fused step began to change state (FusedAdamWStepFailed)
+        propagates: torch's step is run only when nothing has been changed yet."""
 
         if self.use_triton:
             try:
@@ -510,6 +546,8 @@ class AdamWStepWithFallback:
                 else:
                     triton_clip_grad_norm_and_step(optimizer, max_grad_norm)
                 return
+            except FusedAdamWStepFailed:
+                raise
             except Exception as error:
                 if not self._fallback_warned:
                     warnings.warn(
@@ -528,12 +566,15 @@ class AdamWStepWithFallback:
         """The train loop's fp16 update (reference src/picotron/training/train_loop.py:155-160):
         ``grad_scaler.unscale_``, ``clip_grad_norm_`` when ``max_grad_norm`` is given,
         ``grad_scaler.step`` and ``grad_scaler.update``; fused on the fast path
-        (:func:`triton_grad_scaler_step`), else exactly that torch sequence."""
+        (:func:`triton_grad_scaler_step`), else exactly that torch sequence (not after an
+        error raised once the fused update began: FusedAdamWStepFailed propagates)."""
 
         if self.use_triton:
             try:
                 triton_grad_scaler_step(grad_scaler, optimizer, max_grad_norm)
                 return
+            except FusedAdamWStepFailed:
+                raise
             except Exception as error:
                 if not self._fallback_warned:
                     warnings.warn(

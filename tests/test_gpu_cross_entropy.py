@@ -28,11 +28,11 @@ TARGET_ATOL_FP32 = 2.0**-21
 
 def _grad_close(grad, ref, n_valid, dtype):
     # d loss/d logits = (softmax - onehot) / n_valid: compare (softmax - onehot) so the
-    # relative tolerance of the storage type applies to O(1/V)..O(1) values.  (fp16 gradients
-    # are checked at a realistic loss scale instead, in _check and
-    # test_fp16_gradients_at_training_scale.)
-    rtol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]
-    atol = {torch.float32: 1e-9, torch.float16: 2.0**-25 * n_valid + 1e-9, torch.bfloat16: 1e-7}[dtype]
+    # relative tolerance of the storage type applies to O(1/V)..O(1) values.  fp16 gradients
+    # exist only at a loss scale and are checked there (_fp16_grad_close).
+    assert dtype in (torch.float32, torch.bfloat16), "fp16 gradients: use _fp16_grad_close"
+    rtol = {torch.float32: 1e-5, torch.bfloat16: 1.6e-2}[dtype]
+    atol = {torch.float32: 1e-9, torch.bfloat16: 1e-7}[dtype]
     a, e = grad.double() * n_valid, ref.double() * n_valid
     if dtype == torch.float32 and e.numel() > 0:
         tol = rtol * e.abs() + torch.where(e < 0, TARGET_ATOL_FP32, atol)
@@ -43,6 +43,22 @@ def _grad_close(grad, ref, n_valid, dtype):
             f"{float(e.flatten()[worst])} (tolerance {float(tol.flatten()[worst])})")
     else:
         torch.testing.assert_close(a, e, rtol=rtol, atol=atol)
+
+
+def _fp16_scale_for(n_valid: int) -> float:
+    """A GradScaler-sized loss gradient: the initial 2^16, halved for a single valid row,
+    whose target entry (softmax_t - 1) * g would otherwise round past fp16's largest finite
+    value (in torch's path as well: GradScaler would then back off)."""
+
+    return 65536.0 if n_valid > 1 else 32768.0
+
+
+def _fp16_grad_close(grad, ref_grad, scale):
+    # fp16 gradient written at a loss scale: relative bound 2e-3 with a floor of one fp16
+    # subnormal step (2^-24), independent of the row count
+    ref = ref_grad.to(grad.device).double() * scale
+    excess = (grad.double() - ref).abs() - (2e-3 * ref.abs() + 2.0 ** -24)
+    assert float(excess.max()) <= 0, f"fp16 gradient: max excess {float(excess.max())}"
 
 
 def _loss_only_streams(logits, dtype) -> bool:
@@ -77,14 +93,9 @@ def _check(logits, targets, dtype):
         # softmax / n_valid is mostly below fp16's subnormals in the reference as well):
         # relative bound with a floor of one fp16 subnormal step, independent of n_valid
         assert torch.equal(buf, logits)
-        # GradScaler's initial 2^16, halved for a single valid row, whose target entry
-        # (softmax_t - 1) * g would otherwise round past fp16's largest finite value (in
-        # torch's path as well: GradScaler would then back off)
-        g = 65536.0 if n_valid > 1 else 32768.0
+        g = _fp16_scale_for(n_valid)
         ops.cross_entropy_scale_grad(buf, targets, torch.full((), g, device=logits.device), workspace=ws)
-        ref = ref_grad.to(buf.device) * g
-        excess = (buf.double() - ref).abs() - (2e-3 * ref.abs() + 2.0 ** -24)
-        assert float(excess.max()) <= 0, f"fp16 gradient: max excess {float(excess.max())}"
+        _fp16_grad_close(buf, ref_grad, g)
     else:
         # the backward for a grad_output of 1 leaves fp32 / bf16 rows as the forward wrote them
         ops.cross_entropy_scale_grad(buf, targets, torch.ones((), device=logits.device), workspace=ws)

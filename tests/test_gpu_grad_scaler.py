@@ -135,3 +135,64 @@ def test_already_unscaled_optimizer_is_rejected_untouched(gpu):
     sc_f.update()
     _reference_step(sc_r, opt_r, ref, None)
     _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=True)
+
+
+def test_a_failure_after_the_update_began_is_not_retried_by_the_fallback(gpu, monkeypatch):
+    # A launch error inside the fused update (here forced from the host by replacing the step
+    # launcher) comes after the step counters were advanced and the gradients unscaled:
+    # running torch's unscale_ / step again would unscale twice and count the step twice, so
+    # the error propagates and nothing is applied a second time.
+    from picotron_amd import _lib, ops
+    from picotron_amd.nn.triton_kernels import FusedAdamWStepFailed
+
+    fused, _, opt_f, _, sc_f, _ = _setup(gpu, 300)
+    _set_grads(fused, fused, gpu, 301, sc_f.get_scale())
+    hook = AdamWStepWithFallback(use_triton=True)
+    hook.step_with_grad_scaler(sc_f, opt_f, max_grad_norm=1.0)  # one good step: state exists
+    torch.cuda.synchronize()
+    params_before = [p.detach().clone() for p in fused]
+    steps_before = [float(opt_f.state[p]["step"]) for p in fused[:-1]]
+    scale_before = sc_f.get_scale()
+    _set_grads(fused, fused, gpu, 302, scale_before)
+
+    def failing_launch(*args, **kwargs):
+        raise _lib.HipKernelError("pt_adamw_step_scaled", _lib.PT_ELAUNCH, "forced by the test")
+
+    monkeypatch.setattr(ops, "adamw_step_scaled", failing_launch)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # no fallback warning either
+        with pytest.raises(FusedAdamWStepFailed):
+            hook.step_with_grad_scaler(sc_f, opt_f, max_grad_norm=1.0)
+    torch.cuda.synchronize()
+    # the counters advanced once (by the fused path, before its launch failed), not twice
+    assert [float(opt_f.state[p]["step"]) for p in fused[:-1]] == [s + 1 for s in steps_before]
+    # no update was applied, by the fused kernel or by torch's step
+    for p, before in zip(fused, params_before):
+        assert torch.equal(p.detach(), before)
+
+
+def test_a_failure_after_the_plain_step_began_is_not_retried(gpu, monkeypatch):
+    from picotron_amd import _lib, ops
+    from picotron_amd.nn.triton_kernels import FusedAdamWStepFailed
+
+    fused, _, opt_f, _, _, _ = _setup(gpu, 400)
+    _set_grads(fused, fused, gpu, 401, 1.0)
+    hook = AdamWStepWithFallback(use_triton=True)
+    hook.step(opt_f)
+    torch.cuda.synchronize()
+    params_before = [p.detach().clone() for p in fused]
+    steps_before = [float(opt_f.state[p]["step"]) for p in fused[:-1]]
+
+    def failing_launch(*args, **kwargs):
+        raise _lib.HipKernelError("pt_adamw_step", _lib.PT_ELAUNCH, "forced by the test")
+
+    monkeypatch.setattr(ops, "adamw_step", failing_launch)
+    with pytest.raises(FusedAdamWStepFailed):
+        hook.step(opt_f)
+    assert [float(opt_f.state[p]["step"]) for p in fused[:-1]] == [s + 1 for s in steps_before]
+    for p, before in zip(fused, params_before):
+        assert torch.equal(p.detach(), before)
+    # an optimizer the fused path rejects before changing anything still falls back
+    sgd = torch.optim.SGD([fused[0]], lr=0.1)
+    with pytest.warns(RuntimeWarning):
+        AdamWStepWithFallback(use_triton=True).step(sgd)

@@ -95,3 +95,39 @@ def test_partials_beyond_the_scratch_are_rejected_before_launch(gpu):
     assert rc == _lib.PT_EUNSUPPORTED
     message = _lib.lib().pt_last_error().decode()
     assert "static scratch" in message and str(need) in message
+
+
+def test_replays_of_a_captured_call_match_the_workspace_entry_point(gpu):
+    # The first call on a device looks up the scratch's address (and is refused inside a
+    # capture), so one eager call comes first; the captured call then replays on new inputs
+    # written by eager work between the replays.
+    rows, cols = 4096, 4096
+    x, dy, w, rstd = _inputs(rows, cols, torch.bfloat16, torch.bfloat16, gpu, 41)
+    dx = torch.empty_like(x)
+    dw = torch.empty(cols, dtype=w.dtype, device=gpu)
+    stream = torch.cuda.Stream()
+
+    def call():
+        _lib.call(
+            "pt_rmsnorm_bwd_noalloc",
+            dy.data_ptr(), cols, x.data_ptr(), cols, w.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+            cols, dw.data_ptr(), rows, cols, _lib.PT_BFLOAT16, _lib.PT_BFLOAT16,
+            torch.cuda.current_stream(gpu).cuda_stream,
+        )
+
+    call()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        call()
+    for replay in range(3):
+        xn, dyn, _, _ = _inputs(rows, cols, torch.bfloat16, torch.bfloat16, gpu, 50 + replay)
+        x.copy_(xn)
+        dy.copy_(dyn)
+        _, r = ops.rmsnorm_fwd(x, w, 1e-5)
+        rstd.copy_(r)
+        dx_ref, dw_ref = ops.rmsnorm_bwd(dy, x, w, rstd)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dx, dx_ref), f"replay {replay}: dx"
+        assert torch.equal(dw, dw_ref), f"replay {replay}: dW"
