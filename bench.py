@@ -126,42 +126,45 @@ class RMSNormWorkload(Workload):
     name = "rmsnorm"
     metric = HEADLINE_METRIC
     rows, cols, eps = 16384, 4096, 1e-5
+    storage = torch.bfloat16  # activations and weight
 
     def __init__(self, layers: int) -> None:
         self.layers = layers
         self.launches_per_step = layers
-        r, c = self.rows, self.cols
-        self.w = _seeded((c,), torch.bfloat16, 2, 0.02, 1.0)
-        self.x = [_seeded((r, c), torch.bfloat16, 10 + i) for i in range(layers)]
-        self.dy = [_seeded((r, c), torch.bfloat16, 20 + i) for i in range(layers)]
+        r, c, st = self.rows, self.cols, self.storage
+        code = ops.dtype_code(st)
+        self.w = _seeded((c,), st, 2, 0.02, 1.0)
+        self.x = [_seeded((r, c), st, 10 + i) for i in range(layers)]
+        self.dy = [_seeded((r, c), st, 20 + i) for i in range(layers)]
         self.y = [torch.empty_like(t) for t in self.x]
         self.dx = [torch.empty_like(t) for t in self.x]
         self.rstd = [torch.empty(r, dtype=torch.float32, device="cuda") for _ in range(layers)]
-        self.dw = [torch.empty(c, dtype=torch.bfloat16, device="cuda") for _ in range(layers)]
+        self.dw = [torch.empty(c, dtype=st, device="cuda") for _ in range(layers)]
         lib = _lib.lib()
-        self.ws_bytes = lib.pt_rmsnorm_bwd_workspace_bytes(r, c, _lib.PT_BFLOAT16)
+        self.ws_bytes = lib.pt_rmsnorm_bwd_workspace_bytes(r, c, code)
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device="cuda")
-        s, sw = 2, 2
+        s = sw = torch.tensor([], dtype=st).element_size()
         self.fwd_bytes = 2 * r * c * s + c * sw + 4 * r
         self.bwd_bytes = 3 * r * c * s + 2 * c * sw + 4 * r
         self.bytes_per_step = layers * (self.fwd_bytes + self.bwd_bytes)
         self.tokens_per_step = layers * r
         self.dominant = "rmsnorm backward (rmsnorm_bwd_kernel row pass + rmsnorm_dw_finish_kernel)"
         self.dominant_bytes = self.bwd_bytes
+        tname = {torch.bfloat16: "bf16", torch.float32: "fp32"}[st]
         self.description = (
-            f"RMSNorm fwd+bwd bf16 [16384 tokens (8x2048), 4096], eps 1e-5, bf16 weight, fp32 rstd; "
+            f"RMSNorm fwd+bwd {tname} [16384 tokens (8x2048), 4096], eps 1e-5, {tname} weight, fp32 rstd; "
             f"step = forward of {layers} independent activations then backward in reverse"
         )
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         self._fwd = [
             (lib.pt_rmsnorm_fwd, (_p(self.x[i]), c, _p(self.w), _p(self.y[i]), c, _p(self.rstd[i]),
-                                  r, c, ctypes.c_float(self.eps), _lib.PT_BFLOAT16, _lib.PT_BFLOAT16, stream))
+                                  r, c, ctypes.c_float(self.eps), code, code, stream))
             for i in range(layers)
         ]
         self._bwd = [
             (lib.pt_rmsnorm_bwd, (_p(self.dy[i]), c, _p(self.x[i]), c, _p(self.w), _p(self.rstd[i]),
                                   _p(self.dx[i]), c, _p(self.dw[i]), _p(self.ws), self.ws_bytes, r, c,
-                                  _lib.PT_BFLOAT16, _lib.PT_BFLOAT16, stream))
+                                  code, code, stream))
             for i in range(layers)
         ]
 
@@ -228,14 +231,25 @@ class RMSNormWorkload(Workload):
         x, dy, w = self.x[0].cpu(), self.dy[0].cpu(), self.w.cpu()
         sec, calls = _time_cpu(lambda: o_rms.fallback_forward_backward(x, w, self.eps, dy))
         c = self.cols
-        nbytes = 5 * rows * c * 2 + 3 * c * 2 + 8 * rows
+        s = x.element_size()
+        nbytes = 5 * rows * c * s + 3 * c * s + 8 * rows
         return dict(
             value=nbytes / sec / 1e9, unit="GB/s", cores=cores, kind="port",
             sample=f"one activation [{rows}, {c}] (one of the step's {self.layers} layers): reference PyTorch "
-                   f"fallback fwd+bwd (rmsnorm.py:56-60,113-134) on bf16 CPU tensors, median of {calls} calls "
-                   f"(~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+                   f"fallback fwd+bwd (rmsnorm.py:56-60,113-134) on {x.dtype} CPU tensors, median of {calls} "
+                   f"calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=rows / sec,
         )
+
+
+class RMSNormFp32Workload(RMSNormWorkload):
+    """RMSNorm at the headline shape in fp32, the storage type the decoder feeds its norms in
+    training (picotron_decoder.py:116-123,186: the residual stream stays fp32)."""
+
+    name = "rmsnorm_fp32"
+    metric = "RMSNorm fwd+bwd HBM GB/s & % of peak, 16k tok x 4096 fp32"
+    dtype = "f32"
+    storage = torch.float32
 
 
 class ResidualRMSNormWorkload(Workload):
@@ -528,22 +542,41 @@ def _host_time(step, steps: int, warmup: int = 2) -> float:
     return (time.perf_counter() - t0) / steps
 
 
+# Whether the secondary lines get their CPU baseline (off with --no-cpu-baseline).
+_WITH_CPU_BASELINE = True
+
+OTHER_CONFIGS = ("rope", "ce", "ce_ref_call", "adamw", "adamw_list", "rmsnorm_fp32")
+
+
 def _other_configs(steps: int) -> dict:
-    """RoPE (q [8,2048,32,128] + k [8,2048,8,128], rotate-half, 4 layers), the fused
-    cross-entropy ([8192, 128256] bf16) and the fused AdamW step (1.2e9 fp32 parameters, as one
-    tensor and as 100):
-    each built, timed by the host clock over ``steps`` steps after 2 warm-ups, and freed."""
+    """The other configurations, each built, measured like the headline (host-clock value,
+    HIP events per dominant launch, HBM traffic from its committed counter summary, CPU
+    baseline on a bounded sample) and freed: RoPE (q [8,2048,32,128] + k [8,2048,8,128],
+    rotate-half, 4 layers), the fused cross-entropy ([8192, 128256] bf16, in place), the
+    reference's unchanged train-loop call ([4, 2049, 128256] bf16, out of place), the fused
+    AdamW step (1.2e9 fp32 parameters, as one tensor and as 100) and RMSNorm in fp32, the
+    norms' training dtype ([16384, 4096], 4 layers)."""
 
     out = {}
-    for name in ("rope", "ce", "adamw", "adamw_list"):
+    for name in OTHER_CONFIGS:
         wl = WORKLOADS[name](DEFAULT_LAYERS[name])
-        sec = _host_time(wl.step, steps)
+        m = _measure(wl, name, steps, warmup=2)
+        sec = m["elapsed"] / steps
         gbps = wl.bytes_per_step / sec / 1e9
+        dom = m["per_kernel"][m["dominant"]]
         out[name] = {
             "workload": wl.description,
             "ms_per_step": round(sec * 1e3, 4),
             "gbs": round(gbps, 1),
             "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+            "kernel": dom["kernel"],
+            "algorithmic_bytes_per_launch": dom["algorithmic_bytes_per_launch"],
+            "avg_launch_us": dom["avg_launch_us"],
+            "achieved": dom["achieved"],
+            "frac": dom["frac"],
+            "traffic": dom["traffic"],
+            "traffic_source": m["traffic_source"],
+            "cpu_baseline": _cpu_line(wl) if _WITH_CPU_BASELINE else None,
         }
         del wl
         torch.cuda.empty_cache()
@@ -655,7 +688,8 @@ class CrossEntropyWorkload(Workload):
             "previous step's in-place output as its logits)"
         )
         self._call = (lib.pt_cross_entropy, (_p(self.logits), r, 1, v, 0, v, _p(self.targets), 1, 0, -100,
-                                             _p(self.loss), 1, _p(self.ws), self.ws_bytes, _lib.PT_BFLOAT16, stream))
+                                             _p(self.loss), 1, None, 0, 0, _p(self.ws), self.ws_bytes,
+                                             _lib.PT_BFLOAT16, stream))
 
     def step(self, events):
         fn, args = self._call
@@ -783,6 +817,43 @@ class CrossEntropyTrainWorkload(Workload):
                    f"calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=self.b * (s - 1) / sec,
         )
+
+
+class CrossEntropyReferenceCallWorkload(CrossEntropyTrainWorkload):
+    """The train loop's loss call exactly as the reference writes it (train_loop.py:95-97,
+    141-144): ``CrossEntropyWithFallback(use_triton=True)`` (drop-in default: the logits are
+    left untouched) on ``logits[:, :-1, :].transpose(1, 2)`` against ``input_ids[:, 1:]``, then
+    the backward.  The kernel reads the logits and writes the gradient into a new buffer; the
+    view is computed on its base, so autograd runs no slice backward."""
+
+    name = "ce_ref_call"
+    metric = ("Next-token cross-entropy fwd + autograd bwd through the reference's call site, "
+              "HBM GB/s & % of peak, logits [4, 2049, 128256] bf16")
+
+    def __init__(self, layers: int) -> None:
+        from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback
+
+        super().__init__(layers)
+        self.loss_function = CrossEntropyWithFallback(use_triton=True)
+        b, s, v = self.b, self.s, self.vocab
+        self.dominant = ("cross-entropy of the reference's call: logits read, gradient written to a new "
+                         "buffer (ce_prepare_kernel + ce_rows_kernel + ce_finish_kernel; the backward's "
+                         "ce_scale_kernel returns at once for grad 1)")
+        self.description = (
+            f"the reference's train-loop call on model logits [{b}, {s}, {v}] bf16 ~N(0,2^2): "
+            f"CrossEntropyWithFallback(use_triton=True)(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:]) "
+            f"(5% = -100) then torch.autograd.grad to the logits' leaf; the logits are left untouched and "
+            f"the gradient goes to a new buffer"
+        )
+
+    def _step(self, shifted: bool):
+        logits = self.leaf.view(self.b, self.s, self.vocab)
+        loss = self.loss_function(logits[:, :-1, :].transpose(1, 2), self.ids[:, 1:])
+        (grad,) = torch.autograd.grad(loss, self.leaf)
+        return grad
+
+    def extra(self, steps: int) -> dict | None:
+        return None
 
 
 class CrossEntropyTrainFp16Workload(CrossEntropyTrainWorkload):
@@ -1495,11 +1566,13 @@ class CopyWorkload(Workload):
 WORKLOADS = {
     "headline": HeadlineWorkload,
     "rmsnorm": RMSNormWorkload,
+    "rmsnorm_fp32": RMSNormFp32Workload,
     "residual_rmsnorm": ResidualRMSNormWorkload,
     "swiglu": SwiGLUWorkload,
     "rope": RoPEWorkload,
     "ce": CrossEntropyWorkload,
     "ce_train": CrossEntropyTrainWorkload,
+    "ce_ref_call": CrossEntropyReferenceCallWorkload,
     "ce_train_fp16": CrossEntropyTrainFp16Workload,
     "adamw": AdamWWorkload,
     "adamw_list": AdamWListWorkload,
@@ -1510,7 +1583,7 @@ WORKLOADS = {
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "ce_train_fp16": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
+DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "rmsnorm_fp32": 4, "ce_ref_call": 1, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "ce_train_fp16": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
                   "zero_step": 1, "fp16_step": 1, "modules": 1, "copy": 4}
 
 
@@ -1525,69 +1598,40 @@ def _traffic(workload: str) -> dict | None:
     return data
 
 
-def main() -> int:
-    parser = argparse.ArgumentParser(description="fused-kernel HBM benchmark (one MI355X)")
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
-    parser.add_argument("--layers", type=int, default=None)
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-extra", action="store_true",
-                        help="skip the workload's comparison measurements (e.g. the unfused "
-                             "sequence), so that a profile holds only the timed launches")
-    args = parser.parse_args()
+def _measure(wl: Workload, name: str, steps: int, warmup: int) -> dict:
+    """Times ``steps`` steps of ``wl`` after ``warmup`` untimed ones.
 
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the kernels run on a single MI355X and the library has "
-              "no multi-GPU path (run with --gpus 1).", file=sys.stderr)
-        return 2
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        return 2
-    _lib.lib()
-    if not ops.device_supported(0):
-        print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)
-        return 2
+    Pass 1 (the value): nothing but the workload's own launches between two device
+    synchronisations, host clock.  Pass 2 (the roofline): the same steps again with a HIP
+    event pair around every timed launch, recorded on the stream the kernels run on; the
+    event records add a few microseconds per launch, so this pass is not used for the value.
+    A workload with several launch kinds (timed_kinds) gets one event list per kind; the
+    others time their dominant launch.  Per-launch HBM traffic comes from the committed
+    counter summary (profiles/<name>_traffic.json) when there is one."""
 
-    layers = args.layers or DEFAULT_LAYERS[args.workload]
-    wl = WORKLOADS[args.workload](layers)
-    torch.cuda.synchronize()
-
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         wl.step(None)
     torch.cuda.synchronize()
-
-    # Pass 1 (the reported value): K steps, nothing but the workload's own launches between
-    # the two synchronisations.
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         wl.step(None)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
-    # Pass 2 (the roofline): the same K steps again with a HIP event pair around every
-    # timed launch, recorded on the stream the kernels run on.  The event records add a few
-    # microseconds per launch, so this pass is not used for the value.  A workload with
-    # several launch kinds (timed_kinds) gets one event list per kind; the others time their
-    # dominant launch.
     kinds = getattr(wl, "timed_kinds", None)
     if kinds is None:
         kinds = {"dominant": wl.launches_per_step}
     events = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.steps * n)] for k, n in kinds.items()}
+                  for _ in range(steps * n)] for k, n in kinds.items()}
     pending = {k: list(reversed(v)) for k, v in events.items()}
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         wl.step(pending if hasattr(wl, "timed_kinds") else pending["dominant"])
     torch.cuda.synchronize()
     elapsed_instrumented = time.perf_counter() - t1
 
-    ms_per_step = elapsed / args.steps * 1e3
-    gbps = wl.bytes_per_step / (elapsed / args.steps) / 1e9
-    traffic = _traffic(args.workload)
+    traffic = _traffic(name)
     per_kernel = {}
     for kind, pairs in events.items():
         launch_ms = [a.elapsed_time(b) for a, b in pairs]
@@ -1612,7 +1656,13 @@ def main() -> int:
                 entry["traffic"] = per.get("bytes_per_launch")
         per_kernel[kind] = entry
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_ms"])
-    dom = per_kernel[dominant]
+    return dict(elapsed=elapsed, elapsed_instrumented=elapsed_instrumented, per_kernel=per_kernel,
+                dominant=dominant, traffic_source=traffic.get("source") if traffic else None,
+                steps=steps)
+
+
+def _roofline(m: dict) -> dict:
+    dom = m["per_kernel"][m["dominant"]]
     roofline = {
         "bound": "hbm",
         "achieved": dom["achieved"],
@@ -1626,25 +1676,67 @@ def main() -> int:
         "median_launch_us": dom["median_launch_us"],
         "launches_timed": dom["launches_timed"],
         "timing": "HIP events around each launch, in a second pass of the same steps",
-        "ms_per_step_with_events": round(elapsed_instrumented / args.steps * 1e3, 4),
+        "ms_per_step_with_events": round(m["elapsed_instrumented"] / m["steps"] * 1e3, 4),
     }
-    if traffic:
-        roofline["traffic_source"] = traffic.get("source")
-    if len(per_kernel) > 1:
+    if m["traffic_source"]:
+        roofline["traffic_source"] = m["traffic_source"]
+    if len(m["per_kernel"]) > 1:
         roofline["per_kernel"] = {k: {kk: vv for kk, vv in v.items() if kk != "total_ms"}
-                                  for k, v in per_kernel.items()}
+                                  for k, v in m["per_kernel"].items()}
+    return roofline
+
+
+def _cpu_line(wl: Workload) -> dict | None:
+    cpu = wl.cpu_baseline()
+    if cpu is not None:
+        cores, ncpu, model = _cpu_info()
+        cpu.update(os_cpu_count=ncpu, cpu_model=model)
+        for key in ("value", "seconds_per_call", "tokens_per_s", "params_per_s"):
+            if key in cpu:
+                cpu[key] = round(cpu[key], 4) if key == "seconds_per_call" else round(cpu[key], 2)
+    return cpu
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description="fused-kernel HBM benchmark (one MI355X)")
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
+    parser.add_argument("--layers", type=int, default=None)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extra", action="store_true",
+                        help="skip the workload's comparison measurements (e.g. the unfused "
+                             "sequence and the other configurations), so that a profile holds "
+                             "only the timed launches")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the kernels run on a single MI355X and the library has "
+              "no multi-GPU path (run with --gpus 1).", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    _lib.lib()
+    if not ops.device_supported(0):
+        print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)
+        return 2
+
+    global _WITH_CPU_BASELINE
+    _WITH_CPU_BASELINE = not args.no_cpu_baseline
+    layers = args.layers or DEFAULT_LAYERS[args.workload]
+    wl = WORKLOADS[args.workload](layers)
+    torch.cuda.synchronize()
+
+    m = _measure(wl, args.workload, args.steps, args.warmup)
+    elapsed = m["elapsed"]
+    ms_per_step = elapsed / args.steps * 1e3
+    gbps = wl.bytes_per_step / (elapsed / args.steps) / 1e9
+    roofline = _roofline(m)
 
     extra = None if args.no_extra else wl.extra(args.steps)
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = wl.cpu_baseline()
-        if cpu is not None:
-            cores, ncpu, model = _cpu_info()
-            cpu.update(os_cpu_count=ncpu, cpu_model=model)
-            for key in ("value", "seconds_per_call", "tokens_per_s", "params_per_s"):
-                if key in cpu:
-                    cpu[key] = round(cpu[key], 4) if key == "seconds_per_call" else round(cpu[key], 2)
+    cpu = None if args.no_cpu_baseline else _cpu_line(wl)
 
     result = {
         "metric": wl.metric,

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 2
+#define PT_ABI_VERSION 3
 
 /* element type codes (storage types; arithmetic is always fp32) */
 #define PT_FLOAT32 0
@@ -157,13 +157,16 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
  * outer=N, inner=1; the train loop's (B, V, S-1) view of (B, S, V) logits is
  * outer=B, inner=S-1, outer_stride=S*V, inner_stride=V.
  * loss_out (fp32 scalar, device) = sum(lse - logit[target]) / n_valid.
- * If write_grad != 0 the logits are overwritten IN PLACE with
+ * If write_grad != 0, for fp32 and bf16,
  *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows)
- * for fp32 and bf16.  fp16 logits are left unchanged and each row's log-sum-exp is kept in
- * the workspace: the loss scale of fp16 training arrives only with the backward, and
- * softmax / n_valid is mostly below fp16's smallest subnormal at language-model sizes, so
- * pt_cross_entropy_scale_grad (always needed for fp16) writes the gradient, scale included,
- * rounding to fp16 once.
+ * is written in the same pass: with grad == NULL IN PLACE over the logits; otherwise into
+ * the gradient rows grad + o*grad_outer_stride + i*grad_inner_stride (vocab contiguous),
+ * each starting in the same 16-byte phase as its logits row (else PT_EINVAL), and the logits
+ * are only read (one read of the logits and one write of the gradient either way).  fp16
+ * logits are left unchanged and each row's log-sum-exp is kept in the workspace: the loss
+ * scale of fp16 training arrives only with the backward, and softmax / n_valid is mostly
+ * below fp16's smallest subnormal at language-model sizes, so pt_cross_entropy_scale_grad
+ * (always needed for fp16) writes the gradient, scale included, rounding to fp16 once.
  * A non-ignored target outside [0, vocab) makes that row's loss NaN and sets
  * *(int32*)status bit 0; status is part of the workspace (see below).
  * Replaces CrossEntropyWithFallback / triton_cross_entropy
@@ -173,26 +176,30 @@ size_t pt_cross_entropy_workspace_bytes(int64_t rows);
 int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_stride,
                      int64_t inner_stride, int64_t vocab, const int64_t* targets,
                      int64_t t_outer_stride, int64_t t_inner_stride, int64_t ignore_index,
-                     float* loss_out, int write_grad, void* workspace, size_t workspace_bytes,
+                     float* loss_out, int write_grad, void* grad, int64_t grad_outer_stride,
+                     int64_t grad_inner_stride, void* workspace, size_t workspace_bytes,
                      int dtype, void* stream);
 
 /* Device address of the int32 status word inside a cross-entropy workspace. */
 int32_t* pt_cross_entropy_status(void* workspace);
 
-/* Multiply a gradient written by pt_cross_entropy (same row and target description) by
- * the fp32 scalar at *grad_output (device memory), skipping all work when it equals 1.0
- * exactly; rows whose target is ignore_index stay zero.  This is the backward of the fused
- * loss: the logits already hold d(mean loss)/d(logits).  For fp16 the logits are still the
- * logits and each element becomes (exp(x - lse) - onehot) * (*grad_output / n_valid), computed
- * in fp32 and rounded to fp16 once (always, also for a grad_output of 1); lse and n_valid are
- * read from `workspace`, the forward call's workspace, which must then be non-NULL (fp32 and
- * bf16 ignore it). */
-int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
+/* The backward of the fused loss.  `dlogits` (strides outer_stride, inner_stride) are the
+ * gradient rows pt_cross_entropy wrote (the logits themselves when it worked in place; same
+ * targets): multiplied in place by the fp32 scalar at *grad_output (device memory), all work
+ * skipped when it equals 1.0 exactly; rows whose target is ignore_index stay zero.  For fp16
+ * the gradient is written here: each element of the untouched logits, at `logits` (strides
+ * logits_outer_stride, logits_inner_stride; NULL: dlogits, in place, the ABI-2 behaviour),
+ * gives (exp(x - lse) - onehot) * (*grad_output / n_valid) in dlogits, computed in fp32 and
+ * rounded to fp16 once (always, also for a grad_output of 1), each logits row in the same
+ * 16-byte phase as its gradient row; lse and n_valid are read from `workspace`, the forward
+ * call's workspace, which must then be non-NULL (fp32 and bf16 ignore `logits` and it). */
+int pt_cross_entropy_scale_grad(void* dlogits, int64_t outer, int64_t inner,
                                 int64_t outer_stride, int64_t inner_stride, int64_t vocab,
                                 const int64_t* targets, int64_t t_outer_stride,
                                 int64_t t_inner_stride, int64_t ignore_index,
-                                const float* grad_output, const void* workspace, int dtype,
-                                void* stream);
+                                const float* grad_output, const void* logits,
+                                int64_t logits_outer_stride, int64_t logits_inner_stride,
+                                const void* workspace, int dtype, void* stream);
 
 /* Next-token cross-entropy on the whole (batch, seq, vocab) logits of a language model:
  * row (b, t) with t < seq-1 has target input_ids[b*ids_batch_stride + (t+1)*ids_seq_stride];
@@ -202,22 +209,25 @@ int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
  * at src/picotron/training/train_loop.py:141-144 -- but with write_grad the gradient
  * covers the whole (batch, seq, vocab) buffer, so autograd needs no slice backward (which
  * allocates, zero-fills and copies a full-size gradient).  Row (b, t) starts at
- * logits + b*batch_stride + t*seq_stride.  Workspace:
- * pt_cross_entropy_workspace_bytes(batch * seq). */
+ * logits + b*batch_stride + t*seq_stride; with grad != NULL the gradient goes to
+ * grad + b*grad_batch_stride + t*grad_seq_stride instead of over the logits (same rule as
+ * pt_cross_entropy).  Workspace: pt_cross_entropy_workspace_bytes(batch * seq). */
 int pt_cross_entropy_shifted(void* logits, int64_t batch, int64_t seq, int64_t batch_stride,
                              int64_t seq_stride, int64_t vocab, const int64_t* input_ids,
                              int64_t ids_batch_stride, int64_t ids_seq_stride,
-                             int64_t ignore_index, float* loss_out, int write_grad,
+                             int64_t ignore_index, float* loss_out, int write_grad, void* grad,
+                             int64_t grad_batch_stride, int64_t grad_seq_stride,
                              void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
 /* pt_cross_entropy_scale_grad for a gradient written by pt_cross_entropy_shifted (same
  * description, same fp16 rule and workspace); the last position and ignored rows stay zero. */
-int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq,
+int pt_cross_entropy_shifted_scale_grad(void* dlogits, int64_t batch, int64_t seq,
                                         int64_t batch_stride, int64_t seq_stride, int64_t vocab,
                                         const int64_t* input_ids, int64_t ids_batch_stride,
                                         int64_t ids_seq_stride, int64_t ignore_index,
-                                        const float* grad_output, const void* workspace,
-                                        int dtype, void* stream);
+                                        const float* grad_output, const void* logits,
+                                        int64_t logits_batch_stride, int64_t logits_seq_stride,
+                                        const void* workspace, int dtype, void* stream);
 
 /* ---------------------------------------------------------------- AdamW
  * One decoupled-weight-decay Adam step over many fp32 tensors in one launch, with

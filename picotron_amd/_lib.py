@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("PICOTRON_HIP_LIB", Path(__file__).with_name("libpicotron_hip.so")))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 PT_FLOAT32 = 0
 PT_FLOAT16 = 1
@@ -74,23 +74,25 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pt_cross_entropy": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
-         c_int64, c_void_p, c_int, c_void_p, c_size_t, c_int, c_void_p],
+         c_int64, c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_size_t, c_int,
+         c_void_p],
     ),
     "pt_cross_entropy_status": (c_void_p, [c_void_p]),
     "pt_cross_entropy_scale_grad": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
-         c_int64, c_void_p, c_void_p, c_int, c_void_p],
+         c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int, c_void_p],
     ),
     "pt_cross_entropy_shifted": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
-         c_int64, c_void_p, c_int, c_void_p, c_size_t, c_int, c_void_p],
+         c_int64, c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p, c_size_t, c_int,
+         c_void_p],
     ),
     "pt_cross_entropy_shifted_scale_grad": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64,
-         c_int64, c_void_p, c_void_p, c_int, c_void_p],
+         c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int, c_void_p],
     ),
     "pt_adamw_block_elems": (c_int64, []),
     "pt_adamw_step": (

@@ -1,4 +1,6 @@
-// Fused cross-entropy (mean over non-ignored rows) with its gradient written in place.
+// Fused cross-entropy (mean over non-ignored rows) with its gradient written in place, over
+// the logits, or into a separate gradient buffer whose rows lie in the same 16-byte phase as
+// the logits rows (the logits are then only read).
 //
 // Reference semantics (AndyMLAndAI/picotron):
 //   src/picotron/nn/triton_kernels/cross_entropy.py:97-109 -> F.cross_entropy(logits,
@@ -131,22 +133,25 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
 // status bit 0) before any thread of the block can overwrite the row: the block passes at
 // least two barriers before its first gradient store.
 template <typename T, int V, bool ALIGNED>
-__device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t valid_inner,
-                                             int64_t os, int64_t is, int vocab,
+__device__ __forceinline__ bool ce_row_begin(const T* logits, T* grad, int64_t inner,
+                                             int64_t valid_inner, int64_t os, int64_t is,
+                                             int64_t gos, int64_t gis, int vocab,
                                              const int64_t* targets, int64_t tos, int64_t tis,
                                              int64_t ignore_index, int write_grad, CeWork* ws,
-                                             T** p_out, int* tgt_out, float* s_target_logit) {
+                                             const T** p_out, T** g_out, int* tgt_out,
+                                             float* s_target_logit) {
   const int64_t row = blockIdx.x;
   const int64_t o = row / inner, ii = row - (row / inner) * inner;
-  T* p = logits + o * os + ii * is;
+  const T* p = logits + o * os + ii * is;
+  T* g = grad + o * gos + ii * gis;
   const int64_t tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
   if (tgt == ignore_index) {
     if (write_grad == kGradWrite) {
       for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
         if constexpr (ALIGNED) {
-          store16<true>(p + e, u32x4{0u, 0u, 0u, 0u});
+          store16<true>(g + e, u32x4{0u, 0u, 0u, 0u});
         } else {
-          p[e] = Elem<T>::from_f32(0.0f);
+          g[e] = Elem<T>::from_f32(0.0f);
         }
       }
     }
@@ -159,6 +164,7 @@ __device__ __forceinline__ bool ce_row_begin(T* logits, int64_t inner, int64_t v
     if (bad) atomicOr(&ws->status, 1);
   }
   *p_out = p;
+  *g_out = g;
   *tgt_out = bad ? -1 : static_cast<int>(tgt);
   return true;
 }
@@ -183,7 +189,8 @@ __device__ __forceinline__ float target_grad(float mx, float se, float xt, float
 // Where a row lives and what its target is; uniform across the block.  A row without a
 // target (ignore_index, or a position i >= valid_inner) has skip set.
 struct RowRef {
-  int64_t off;
+  int64_t off;   // of the logits row
+  int64_t goff;  // of its gradient row
   int64_t tgt;
   bool skip;
 };
@@ -191,10 +198,12 @@ struct RowRef {
 __device__ __forceinline__ RowRef row_ref(int64_t row, int64_t inner, int64_t valid_inner,
                                           int64_t os, int64_t is,
                                           const int64_t* __restrict__ targets, int64_t tos,
-                                          int64_t tis, int64_t ignore_index) {
+                                          int64_t tis, int64_t ignore_index, int64_t gos = 0,
+                                          int64_t gis = 0) {
   const int64_t o = row / inner, ii = row - o * inner;
   RowRef r;
   r.off = o * os + ii * is;
+  r.goff = o * gos + ii * gis;
   r.tgt = ii < valid_inner ? targets[o * tos + ii * tis] : ignore_index;
   r.skip = r.tgt == ignore_index;
   return r;
@@ -240,9 +249,9 @@ constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000
 // inside it.
 template <typename T, int VPT>
 __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
-    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
-    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
+    const T* logits, T* grad, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int64_t gos, int64_t gis, int vocab, const int64_t* __restrict__ targets, int64_t tos,
+    int64_t tis, int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
   constexpr int kChunkBytes = kThreads * 16;
   __shared__ float red_m[kWaves];
@@ -252,14 +261,16 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   const int64_t row = blockIdx.x;
   const int row_bytes = vocab * static_cast<int>(sizeof(T));
   const int voff = tid * 16;
-  const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
-  const auto buf = row_buffer(logits + cur.off, row_bytes);
+  const RowRef cur =
+      row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index, gos, gis);
+  const auto buf = row_buffer(const_cast<T*>(logits) + cur.off, row_bytes);
+  const auto gbuf = row_buffer(grad + cur.goff, row_bytes);
 
   if (cur.skip) {
     if (write_grad == kGradWrite) {
 #pragma unroll
       for (int k = 0; k < VPT; ++k)
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf,
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, gbuf,
                                                voff + k * kChunkBytes, 0, kNonTemporal);
     }
     if (tid == 0) row_losses(ws)[row] = 0.0f;
@@ -355,17 +366,17 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     // One add per store rather than sixteen offsets held in registers across the row.
     int vo = voff + k * kChunkBytes;
     asm volatile("" : "+v"(vo));
-    __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, vo, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kNonTemporal);
   }
   if (!bad && tid == owner) {
     Vec16<T> one;
     one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n_of(ws)));
     const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
     if constexpr (sizeof(T) == 4) {
-      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kNonTemporal);
     } else {
       __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
-                                            buf, toff, 0, kNonTemporal);
+                                            gbuf, toff, 0, kNonTemporal);
     }
   }
 }
@@ -480,9 +491,9 @@ constexpr int kKeepChunks = 12;
 
 template <typename T, int KEEP>
 __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
-    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
-    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
+    const T* logits, T* grad, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int64_t gos, int64_t gis, int vocab, const int64_t* __restrict__ targets, int64_t tos,
+    int64_t tis, int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = Elem<T>::VEC;
   constexpr int kChunkBytes = kThreads * 16;
   __shared__ float red_m[kWaves];
@@ -491,8 +502,10 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
   const int64_t row = blockIdx.x;
-  const RowRef cur = row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index);
-  T* p = logits + cur.off;
+  const RowRef cur =
+      row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index, gos, gis);
+  const T* p = logits + cur.off;
+  T* g = grad + cur.goff;  // in the same 16-byte phase as p (checked on the host)
   // head [0, head), body [head, head + nbody * V), tail [head + nbody * V, vocab)
   const int lead = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T));
   const int head = lead < vocab ? lead : vocab;
@@ -500,7 +513,8 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   const int tail_start = head + nbody * V;
   const int ntail = vocab - tail_start;
   const int body_bytes = nbody * 16;
-  const auto buf = row_buffer(p + head, body_bytes);
+  const auto buf = row_buffer(const_cast<T*>(p) + head, body_bytes);
+  const auto gbuf = row_buffer(g + head, body_bytes);
   const int voff = tid * 16;
   // the one head or tail element of this thread, if any
   const int my_edge = tid < head ? tid : (kThreads - 1 - tid < ntail ? tail_start + (kThreads - 1 - tid) : -1);
@@ -508,9 +522,9 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
   if (cur.skip) {
     if (write_grad == kGradWrite) {
       for (int b = 0; b < body_bytes; b += kChunkBytes)
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, buf, voff + b, 0,
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, gbuf, voff + b, 0,
                                                kNonTemporal);
-      if (my_edge >= 0) p[my_edge] = Elem<T>::from_f32(0.0f);
+      if (my_edge >= 0) g[my_edge] = Elem<T>::from_f32(0.0f);
     }
     if (tid == 0) row_losses(ws)[row] = 0.0f;
     return;
@@ -614,7 +628,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     for (int i = 0; i < V; ++i) out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(kv[k].e[i]) * f);
     int vo = voff + k * kChunkBytes;
     asm volatile("" : "+v"(vo));
-    __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, vo, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kNonTemporal);
   }
   for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
@@ -628,11 +642,11 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
 #pragma unroll
       for (int i = 0; i < V; ++i)
         out.e[i] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(v[u].e[i]), M) * scale);
-      __builtin_amdgcn_raw_buffer_store_b128(out.raw, buf, voff + b + u * kChunkBytes, 0,
+      __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, voff + b + u * kChunkBytes, 0,
                                              kNonTemporal);
     }
   }
-  if (my_edge >= 0) p[my_edge] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(p[my_edge]), M) * scale);
+  if (my_edge >= 0) g[my_edge] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(p[my_edge]), M) * scale);
   if (!bad) {
     // The owner rewrites the target over its own earlier store of that element, through the
     // same kind of access (buffer store for the body, plain store for head and tail), so the
@@ -648,13 +662,13 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
         one.e[0] = gt;
         const int toff = (t - head) * static_cast<int>(sizeof(T));
         if constexpr (sizeof(T) == 4) {
-          __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], buf, toff, 0, kNonTemporal);
+          __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kNonTemporal);
         } else {
           __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
-                                                buf, toff, 0, kNonTemporal);
+                                                gbuf, toff, 0, kNonTemporal);
         }
       } else {
-        p[t] = gt;
+        g[t] = gt;
       }
     }
   }
@@ -664,16 +678,17 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
 // thread; pass 2 re-reads it to write the gradient.
 template <typename T, bool ALIGNED>
 __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
-    T* __restrict__ logits, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
-    int vocab, const int64_t* __restrict__ targets, int64_t tos, int64_t tis,
-    int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
+    const T* logits, T* grad, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
+    int64_t gos, int64_t gis, int vocab, const int64_t* __restrict__ targets, int64_t tos,
+    int64_t tis, int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
   constexpr int V = ALIGNED ? Elem<T>::VEC : 1;
   __shared__ float red[kWaves];
   __shared__ float s_target_logit;
-  T* p = nullptr;
+  const T* p = nullptr;
+  T* g = nullptr;
   int tgt = 0;
-  if (!ce_row_begin<T, V, ALIGNED>(logits, inner, valid_inner, os, is, vocab, targets, tos,
-                                   tis, ignore_index, write_grad, ws, &p, &tgt,
+  if (!ce_row_begin<T, V, ALIGNED>(logits, grad, inner, valid_inner, os, is, gos, gis, vocab,
+                                   targets, tos, tis, ignore_index, write_grad, ws, &p, &g, &tgt,
                                    &s_target_logit))
     return;
 
@@ -718,13 +733,13 @@ __global__ __launch_bounds__(kThreads) void ce_rows_stream_kernel(
   for (int e = threadIdx.x * V; e < vocab; e += kThreads * V) {
     float x[V];
     load(e, x);
-    float g[V];
+    float gv[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) g[i] = (e + i == tgt) ? gt : exp_shifted(x[i], mx) * scale;
+    for (int i = 0; i < V; ++i) gv[i] = (e + i == tgt) ? gt : exp_shifted(x[i], mx) * scale;
     if constexpr (ALIGNED) {
-      store_f32<T, true>(p + e, g, V);
+      store_f32<T, true>(g + e, gv, V);
     } else {
-      p[e] = Elem<T>::from_f32(g[0]);
+      g[e] = Elem<T>::from_f32(gv[0]);
     }
   }
 }
@@ -742,9 +757,10 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
 }
 
 // The backward.  fp32 and bf16: in-place gradient scaling by a device scalar, a no-op when the
-// scalar is exactly 1.  fp16 (deferred gradient): the logits are still the logits, and each
-// element becomes (exp(x - lse) - [j == target]) * (grad_output / n_valid), computed in fp32 and
-// rounded to fp16 once (lse from the forward's workspace).  Ignored rows are zero whatever the
+// scalar is exactly 1.  fp16 (deferred gradient): each element x of the untouched logits
+// (`src`: the gradient rows themselves when in place) gives the gradient element
+// (exp(x - lse) - [j == target]) * (grad_output / n_valid), computed in fp32 and rounded to
+// fp16 once (lse from the forward's workspace).  Ignored rows are zero whatever the
 // scalar is (torch's nll_loss backward leaves them 0).
 // The work items are (row, chunk of 1024 vectors or elements); a grid of up to 128 blocks
 // per CU walks them (a one-shot grid streams no faster and makes the common
@@ -753,10 +769,10 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
 constexpr int kScaleVecs = 4;
 
 template <typename T, bool ALIGNED>
-__global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, int64_t inner,
+__global__ __launch_bounds__(256) void ce_scale_kernel(T* logits, const T* src, int64_t inner,
                                                        int64_t valid_inner, int64_t os,
-                                                       int64_t is, int vocab, int64_t items,
-                                                       int64_t chunks,
+                                                       int64_t is, int64_t sos, int64_t sis,
+                                                       int vocab, int64_t items, int64_t chunks,
                                                        const int64_t* __restrict__ targets,
                                                        int64_t tos, int64_t tis,
                                                        int64_t ignore_index,
@@ -793,6 +809,7 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
     const bool skip = tgt == ignore_index;
     if (!kDefer && skip) continue;
     T* p = logits + o * os + ii * is;
+    const T* q = src + o * sos + ii * sis;  // same 16-byte phase as p (checked on the host)
     // Unaligned rows: a head of elements before the first 16-byte boundary, a body of
     // 16-byte vectors and a tail of fewer than V elements; aligned rows are all body.
     int lead = 0;
@@ -824,8 +841,9 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
     const int cvecs = nbody - cstart < 256 * kScaleVecs ? nbody - cstart : 256 * kScaleVecs;
     const int cbytes = cvecs > 0 ? cvecs * 16 : 0;
     T* cptr = body + static_cast<int64_t>(cstart) * V;
+    const T* qptr = q + lead + static_cast<int64_t>(cstart) * V;
     // an ignored row (deferred gradient) reads nothing: its load resource is empty
-    const auto lbuf = row_buffer(cptr, skip ? 0 : cbytes);
+    const auto lbuf = row_buffer(const_cast<T*>(qptr), skip ? 0 : cbytes);
     const auto sbuf = row_buffer(cptr, cbytes);
     // the target's index in the chunk, or -1 when it is not there (ignored, in another
     // chunk, in the head or tail of an unaligned row, or outside the row)
@@ -868,21 +886,25 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* __restrict__ logits, i
           return Elem<T>::from_f32(y);
         };
         const int t = static_cast<int>(threadIdx.x);
-        if (t < lead) p[t] = fix(p[t], t);
+        if (t < lead) p[t] = fix(q[t], t);
         const int tail = lead + nbody * V + t;
-        if (t < V && tail < vocab) p[tail] = fix(p[tail], tail);
+        if (t < V && tail < vocab) p[tail] = fix(q[tail], tail);
       }
     }
   }
 }
 
-// Row and target description shared by the launches of one call.
+// Row and target description shared by the launches of one call.  `grad` (strides gos, gis)
+// receives the gradient: the logits themselves when in place.  For the backward, `logits`
+// holds the gradient rows and `grad` the rows the fp16 gradient is computed from.
 struct CeRows {
   void* logits;
   int64_t inner, valid_inner, os, is;
   int vocab;
   const int64_t* targets;
   int64_t tos, tis, ignore_index;
+  void* grad;
+  int64_t gos, gis;
 };
 
 // Resident row workgroups per CU (0: no limit); PT_CE_OCCUPANCY overrides it.
@@ -902,8 +924,9 @@ template <typename T, int VPT>
 void launch_rows(const CeRows& d, int write_grad, CeWork* ws, int64_t rows, hipStream_t st) {
   const auto kernel = ce_rows_kernel<T, VPT>;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads),
-                     rows_lds(reinterpret_cast<const void*>(kernel)), st, static_cast<T*>(d.logits),
-                     d.inner, d.valid_inner, d.os, d.is, d.vocab, d.targets, d.tos, d.tis,
+                     rows_lds(reinterpret_cast<const void*>(kernel)), st,
+                     static_cast<const T*>(d.logits), static_cast<T*>(d.grad), d.inner,
+                     d.valid_inner, d.os, d.is, d.gos, d.gis, d.vocab, d.targets, d.tos, d.tis,
                      d.ignore_index, write_grad, ws);
 }
 
@@ -955,8 +978,9 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
   hipLaunchKernelGGL((ce_rows_batched_kernel<T, K>), dim3(static_cast<unsigned>(rows)),        \
                      dim3(kThreads),                                                           \
                      rows_lds(reinterpret_cast<const void*>(ce_rows_batched_kernel<T, K>)), st, \
-                     static_cast<T*>(d.logits), d.inner, d.valid_inner, d.os, d.is, d.vocab,     \
-                     d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws)
+                     static_cast<const T*>(d.logits), static_cast<T*>(d.grad), d.inner,          \
+                     d.valid_inner, d.os, d.is, d.gos, d.gis, d.vocab, d.targets, d.tos, d.tis,  \
+                     d.ignore_index, write_grad, ws)
     if (per_thread <= 1) {
       PT_CE_BATCHED(1);
     } else if (per_thread <= 2) {
@@ -971,15 +995,26 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
 #undef PT_CE_BATCHED
   } else if (aligned) {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
-                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
-                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
-                       ws);
+                       dim3(kThreads), 0, st, static_cast<const T*>(d.logits),
+                       static_cast<T*>(d.grad), d.inner, d.valid_inner, d.os, d.is, d.gos, d.gis,
+                       d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
   } else {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, false>), dim3(static_cast<unsigned>(rows)),
-                       dim3(kThreads), 0, st, static_cast<T*>(d.logits), d.inner, d.valid_inner,
-                       d.os, d.is, d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad,
-                       ws);
+                       dim3(kThreads), 0, st, static_cast<const T*>(d.logits),
+                       static_cast<T*>(d.grad), d.inner, d.valid_inner, d.os, d.is, d.gos, d.gis,
+                       d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
   }
+}
+
+// True when every row of `b` (strides bos, bis) starts in the same 16-byte phase as the
+// matching row of `a` (strides aos, ais): the row kernels split a row at the logits' 16-byte
+// boundaries and address the gradient row with the same offsets.
+bool same_phase(const void* a, int64_t aos, int64_t ais, const void* b, int64_t bos, int64_t bis,
+                int64_t outer, int64_t inner, int esize) {
+  const int64_t base = static_cast<int64_t>(reinterpret_cast<uintptr_t>(b)) -
+                       static_cast<int64_t>(reinterpret_cast<uintptr_t>(a));
+  return base % 16 == 0 && (outer <= 1 || ((bos - aos) * esize) % 16 == 0) &&
+         (inner <= 1 || ((bis - ais) * esize) % 16 == 0);
 }
 
 // The fused loss over outer x inner rows, of which positions i >= valid_inner carry no target.
@@ -999,6 +1034,10 @@ int ce_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_
     return fail(PT_EINVAL, name + ": null pointer");
   if (workspace_bytes < pt_cross_entropy_workspace_bytes(rows) || !aligned16(workspace))
     return fail(PT_EINVAL, name + ": workspace too small or not 16-byte aligned");
+  if (rows > 0 && d.grad != d.logits &&
+      !same_phase(d.logits, d.os, d.is, d.grad, d.gos, d.gis, outer, inner, dtype_size(dtype)))
+    return fail(PT_EINVAL, name + ": gradient rows must start in the same 16-byte phase as the "
+                                  "logits rows");
   hipStream_t st = as_stream(stream);
   CeWork* ws = static_cast<CeWork*>(workspace);
   hipLaunchKernelGGL(ce_prepare_kernel, dim3(1), dim3(kThreads), 0, st, d.targets, d.inner,
@@ -1050,9 +1089,10 @@ void scale_launch_as(const CeRows& d, int64_t rows, const float* grad_output, co
   const auto kernel = ce_scale_kernel<T, ALIGNED>;
   size_t lds = occupancy_lds(per_cu, 0);
   if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
-  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, st, static_cast<T*>(d.logits), d.inner,
-                     d.valid_inner, d.os, d.is, d.vocab, items, chunks, d.targets, d.tos, d.tis,
-                     d.ignore_index, grad_output, ws);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), lds, st, static_cast<T*>(d.logits),
+                     static_cast<const T*>(d.grad), d.inner, d.valid_inner, d.os, d.is, d.gos,
+                     d.gis, d.vocab, items, chunks, d.targets, d.tos, d.tis, d.ignore_index,
+                     grad_output, ws);
 }
 
 template <typename T>
@@ -1077,6 +1117,10 @@ int ce_scale_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, 
     return fail(PT_EINVAL, name + ": null pointer");
   if (dtype == PT_FLOAT16 && (workspace == nullptr || !aligned16(workspace)))
     return fail(PT_EINVAL, name + ": fp16 gradients need the forward's workspace (16-byte aligned)");
+  if (dtype == PT_FLOAT16 && d.grad != d.logits &&
+      !same_phase(d.logits, d.os, d.is, d.grad, d.gos, d.gis, outer, inner, dtype_size(dtype)))
+    return fail(PT_EINVAL, name + ": the logits rows must start in the same 16-byte phase as the "
+                                  "gradient rows");
   const CeWork* ws = static_cast<const CeWork*>(workspace);
   hipStream_t st = as_stream(stream);
   const int esize = dtype_size(dtype);
@@ -1112,62 +1156,80 @@ int32_t* pt_cross_entropy_status(void* workspace) {
 int pt_cross_entropy(void* logits, int64_t outer, int64_t inner, int64_t outer_stride,
                      int64_t inner_stride, int64_t vocab, const int64_t* targets,
                      int64_t t_outer_stride, int64_t t_inner_stride, int64_t ignore_index,
-                     float* loss_out, int write_grad, void* workspace, size_t workspace_bytes,
+                     float* loss_out, int write_grad, void* grad, int64_t grad_outer_stride,
+                     int64_t grad_inner_stride, void* workspace, size_t workspace_bytes,
                      int dtype, void* stream) {
   const int64_t inner_nz = inner > 0 ? inner : 1;
+  const bool out = grad != nullptr;
   const CeRows d{logits, inner_nz, inner_nz, outer_stride, inner_stride,
                  static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
-                 targets, t_outer_stride, t_inner_stride, ignore_index};
+                 targets, t_outer_stride, t_inner_stride, ignore_index,
+                 out ? grad : logits, out ? grad_outer_stride : outer_stride,
+                 out ? grad_inner_stride : inner_stride};
   return ce_run("pt_cross_entropy", d, outer, inner, vocab, loss_out, write_grad, workspace,
                 workspace_bytes, dtype, stream);
 }
 
-int pt_cross_entropy_scale_grad(void* logits, int64_t outer, int64_t inner,
+int pt_cross_entropy_scale_grad(void* dlogits, int64_t outer, int64_t inner,
                                 int64_t outer_stride, int64_t inner_stride, int64_t vocab,
                                 const int64_t* targets, int64_t t_outer_stride,
                                 int64_t t_inner_stride, int64_t ignore_index,
-                                const float* grad_output, const void* workspace, int dtype,
-                                void* stream) {
+                                const float* grad_output, const void* logits,
+                                int64_t logits_outer_stride, int64_t logits_inner_stride,
+                                const void* workspace, int dtype, void* stream) {
   const int64_t inner_nz = inner > 0 ? inner : 1;
-  const CeRows d{logits, inner_nz, inner_nz, outer_stride, inner_stride,
+  const bool out = logits != nullptr && dtype == PT_FLOAT16;
+  const CeRows d{dlogits, inner_nz, inner_nz, outer_stride, inner_stride,
                  static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
-                 targets, t_outer_stride, t_inner_stride, ignore_index};
+                 targets, t_outer_stride, t_inner_stride, ignore_index,
+                 out ? const_cast<void*>(logits) : dlogits,
+                 out ? logits_outer_stride : outer_stride, out ? logits_inner_stride : inner_stride};
   return ce_scale_run("pt_cross_entropy_scale_grad", d, outer, inner, vocab, grad_output,
                       workspace, dtype, stream);
 }
 
 // Rows (b, t) of (batch, seq, vocab) logits; row t < seq - 1 predicts input_ids[b, t + 1], so
-// the targets start one position into input_ids and the last position has none.
+// the targets start one position into input_ids and the last position has none.  `grad`
+// (strides gbs, gss): where the gradient goes (nullptr: over the logits).
 static CeRows shifted_rows(void* logits, int64_t seq, int64_t batch_stride, int64_t seq_stride,
                            int64_t vocab, const int64_t* input_ids, int64_t ids_batch_stride,
-                           int64_t ids_seq_stride, int64_t ignore_index) {
+                           int64_t ids_seq_stride, int64_t ignore_index, void* grad, int64_t gbs,
+                           int64_t gss) {
   const int64_t inner_nz = seq > 0 ? seq : 1;
   const int64_t valid = seq > 1 ? seq - 1 : 0;
   const int64_t* targets = (input_ids != nullptr && valid > 0) ? input_ids + ids_seq_stride : nullptr;
+  const bool out = grad != nullptr;
   return CeRows{logits, inner_nz, valid, batch_stride, seq_stride,
                 static_cast<int>(vocab > 0 && vocab <= (int64_t{1} << 30) ? vocab : 1),
-                targets, ids_batch_stride, ids_seq_stride, ignore_index};
+                targets, ids_batch_stride, ids_seq_stride, ignore_index,
+                out ? grad : logits, out ? gbs : batch_stride, out ? gss : seq_stride};
 }
 
 int pt_cross_entropy_shifted(void* logits, int64_t batch, int64_t seq, int64_t batch_stride,
                              int64_t seq_stride, int64_t vocab, const int64_t* input_ids,
                              int64_t ids_batch_stride, int64_t ids_seq_stride,
-                             int64_t ignore_index, float* loss_out, int write_grad,
+                             int64_t ignore_index, float* loss_out, int write_grad, void* grad,
+                             int64_t grad_batch_stride, int64_t grad_seq_stride,
                              void* workspace, size_t workspace_bytes, int dtype, void* stream) {
   const CeRows d = shifted_rows(logits, seq, batch_stride, seq_stride, vocab, input_ids,
-                                ids_batch_stride, ids_seq_stride, ignore_index);
+                                ids_batch_stride, ids_seq_stride, ignore_index, grad,
+                                grad_batch_stride, grad_seq_stride);
   return ce_run("pt_cross_entropy_shifted", d, batch, seq, vocab, loss_out, write_grad,
                 workspace, workspace_bytes, dtype, stream);
 }
 
-int pt_cross_entropy_shifted_scale_grad(void* logits, int64_t batch, int64_t seq,
+int pt_cross_entropy_shifted_scale_grad(void* dlogits, int64_t batch, int64_t seq,
                                         int64_t batch_stride, int64_t seq_stride, int64_t vocab,
                                         const int64_t* input_ids, int64_t ids_batch_stride,
                                         int64_t ids_seq_stride, int64_t ignore_index,
-                                        const float* grad_output, const void* workspace,
-                                        int dtype, void* stream) {
-  const CeRows d = shifted_rows(logits, seq, batch_stride, seq_stride, vocab, input_ids,
-                                ids_batch_stride, ids_seq_stride, ignore_index);
+                                        const float* grad_output, const void* logits,
+                                        int64_t logits_batch_stride, int64_t logits_seq_stride,
+                                        const void* workspace, int dtype, void* stream) {
+  const bool out = logits != nullptr && dtype == PT_FLOAT16;
+  const CeRows d = shifted_rows(dlogits, seq, batch_stride, seq_stride, vocab, input_ids,
+                                ids_batch_stride, ids_seq_stride, ignore_index,
+                                out ? const_cast<void*>(logits) : nullptr, logits_batch_stride,
+                                logits_seq_stride);
   return ce_scale_run("pt_cross_entropy_shifted_scale_grad", d, batch, seq, vocab, grad_output,
                       workspace, dtype, stream);
 }

@@ -396,12 +396,36 @@ def ce_target_strides(targets: Tensor, outer: int, inner: int) -> tuple[int, int
     raise ValueError("targets shape does not match the logits")
 
 
+def ce_grad_buffer(logits: Tensor, class_dim: int = 1) -> Tensor | None:
+    """An uninitialised tensor of the logits' shape and strides whose data starts in the same
+    16-byte phase as the logits', so that every gradient row starts in the phase of its logits
+    row, as the fused kernels require of a separate gradient (``class_dim``: the contiguous
+    class dimension, 1 for (N, C) and (N, C, d) inputs, 2 for the shifted (B, S, V) form).
+    None when the logits rows overlap in memory (an expanded tensor)."""
+
+    dims = list(zip(logits.shape, logits.stride()))
+    rows = [d for i, d in enumerate(dims) if i != class_dim]
+    if not rows_disjoint(rows, logits.size(class_dim)):
+        return None
+    if logits.numel() == 0:
+        return torch.empty_like(logits)
+    span = 1 + sum((n - 1) * st for n, st in dims)
+    per16 = 16 // logits.element_size()
+    flat = torch.empty(span + per16, dtype=logits.dtype, device=logits.device)
+    offset = ((logits.data_ptr() - flat.data_ptr()) % 16) // logits.element_size()
+    return flat.as_strided(logits.shape, logits.stride(), flat.storage_offset() + offset)
+
+
 def cross_entropy(
-    logits: Tensor, targets: Tensor, ignore_index: int = -100, write_grad: bool = False
+    logits: Tensor, targets: Tensor, ignore_index: int = -100, write_grad: bool = False,
+    grad: Tensor | None = None,
 ) -> tuple[Tensor, Tensor]:
     """Mean cross-entropy (fp32 scalar tensor) over targets != ignore_index.
 
-    With ``write_grad`` the logits are overwritten in place by d(loss)/d(logits).
+    With ``write_grad`` (fp32 and bf16) d(loss)/d(logits) is written in the same pass: into
+    ``grad`` when given (the logits' shape, rows in the logits rows' 16-byte phase, e.g. from
+    :func:`ce_grad_buffer`; the logits are only read), else over the logits in place.  fp16
+    writes its gradient in :func:`cross_entropy_scale_grad`.
     Returns (loss, workspace); the workspace holds the status word (bit 0: a target out
     of range), readable with :func:`cross_entropy_status`.
     """
@@ -409,7 +433,14 @@ def cross_entropy(
     device = _check_cuda(logits, targets)
     outer, inner, os_, is_, vocab = ce_rows(logits)
     tos, tis = ce_target_strides(targets, outer, inner)
-    if write_grad and not rows_disjoint([(outer, os_), (inner, is_)], vocab):
+    gos = gis = 0
+    if grad is not None:
+        if grad.shape != logits.shape or grad.dtype != logits.dtype or grad.device != logits.device:
+            raise ValueError("the gradient buffer must match the logits")
+        _, _, gos, gis, _ = ce_rows(grad)
+        if write_grad and not rows_disjoint([(outer, gos), (inner, gis)], vocab):
+            raise ValueError("cross-entropy gradient rows overlap in memory")
+    elif write_grad and not rows_disjoint([(outer, os_), (inner, is_)], vocab):
         raise ValueError("cross-entropy logits rows overlap in memory; the gradient cannot be "
                          "written into them")
     rows = outer * inner
@@ -419,8 +450,8 @@ def cross_entropy(
     _lib.call(
         "pt_cross_entropy",
         logits.data_ptr(), outer, inner, os_, is_, vocab, targets.data_ptr(), tos, tis,
-        int(ignore_index), loss.data_ptr(), int(write_grad), ws.data_ptr(), ws_bytes,
-        dtype_code(logits.dtype), _stream(device),
+        int(ignore_index), loss.data_ptr(), int(write_grad), _ptr(grad), gos, gis, ws.data_ptr(),
+        ws_bytes, dtype_code(logits.dtype), _stream(device),
     )
     return loss, ws
 
@@ -433,27 +464,36 @@ def cross_entropy_status(ws: Tensor) -> int:
 
 def cross_entropy_scale_grad(
     dlogits: Tensor, targets: Tensor, grad_output: Tensor, ignore_index: int = -100,
-    workspace: Tensor | None = None,
+    workspace: Tensor | None = None, logits: Tensor | None = None,
 ) -> None:
     """dlogits *= grad_output in place (skipped on device when grad_output == 1).  For fp16
     the forward left the logits unchanged and this call writes the gradient,
     (softmax - onehot) * grad_output / n_valid rounded once, from the row log-sum-exps and
-    n_valid in ``workspace`` (the forward's)."""
+    n_valid in ``workspace`` (the forward's): computed from ``logits`` into ``dlogits`` (rows
+    in the same 16-byte phase) when ``logits`` is given, else over ``dlogits`` in place."""
 
     device = _check_cuda(dlogits, targets, grad_output)
     outer, inner, os_, is_, vocab = ce_rows(dlogits)
     tos, tis = ce_target_strides(targets, outer, inner)
+    los = lis = 0
+    if logits is not None:
+        if logits.shape != dlogits.shape or logits.dtype != dlogits.dtype:
+            raise ValueError("logits must match the gradient buffer")
+        _, _, los, lis, _ = ce_rows(logits)
     go = grad_output.detach().to(torch.float32).reshape(())
     _lib.call(
         "pt_cross_entropy_scale_grad",
         dlogits.data_ptr(), outer, inner, os_, is_, vocab, targets.data_ptr(), tos, tis,
-        int(ignore_index), go.data_ptr(), _ptr(workspace), dtype_code(dlogits.dtype),
-        _stream(device),
+        int(ignore_index), go.data_ptr(), _ptr(logits), los, lis, _ptr(workspace),
+        dtype_code(dlogits.dtype), _stream(device),
     )
 
 
-def _shifted_desc(logits: Tensor, input_ids: Tensor) -> tuple[int, int, int, int, int, int, int]:
-    """(batch, seq, batch_stride, seq_stride, vocab, ids_batch_stride, ids_seq_stride)."""
+def _shifted_desc(logits: Tensor, input_ids: Tensor,
+                  next_targets: bool = False) -> tuple[int, int, int, int, int, int, int]:
+    """(batch, seq, batch_stride, seq_stride, vocab, ids_batch_stride, ids_seq_stride).
+    ``next_targets``: ``input_ids`` holds the targets themselves, (batch, seq - 1), entry
+    (b, t) for position t (the train loop's ``input_ids[:, 1:]``)."""
 
     if logits.dim() != 3:
         raise ValueError("shifted cross-entropy logits must be (batch, seq, vocab)")
@@ -462,21 +502,44 @@ def _shifted_desc(logits: Tensor, input_ids: Tensor) -> tuple[int, int, int, int
         raise ValueError("cross-entropy logits need a contiguous vocabulary dimension")
     if input_ids.dtype != torch.long:
         raise ValueError("cross-entropy targets must be int64")
-    if input_ids.dim() != 2 or tuple(input_ids.shape) != (b, s):
-        raise ValueError("input_ids must be (batch, seq) like the logits")
+    want = (b, s - 1) if next_targets else (b, s)
+    if input_ids.dim() != 2 or tuple(input_ids.shape) != want:
+        raise ValueError(f"targets must be {want} for (batch, seq, vocab) logits")
     return b, s, logits.stride(0), logits.stride(1), v, input_ids.stride(0), input_ids.stride(1)
 
 
+def _ids_ptr(input_ids: Tensor, next_targets: bool) -> int:
+    """The address the shifted entry points take as input_ids: they read position t's target
+    at input_ids + (t + 1) * seq_stride, so targets already shifted by one (entry t for
+    position t) are passed as the address one position before them (never dereferenced)."""
+
+    if not next_targets:
+        return input_ids.data_ptr()
+    return input_ids.data_ptr() - input_ids.stride(1) * input_ids.element_size()
+
+
 def cross_entropy_shifted(
-    logits: Tensor, input_ids: Tensor, ignore_index: int = -100, write_grad: bool = False
+    logits: Tensor, input_ids: Tensor, ignore_index: int = -100, write_grad: bool = False,
+    grad: Tensor | None = None, next_targets: bool = False,
 ) -> tuple[Tensor, Tensor]:
     """Next-token mean cross-entropy of (B, S, V) logits against input_ids[:, 1:]: equal to
     :func:`cross_entropy` on ``logits[:, :-1, :].transpose(1, 2)``.  With ``write_grad`` the
-    whole logits buffer is overwritten by d(loss)/d(logits) (last position zero)."""
+    gradient covers the whole (B, S, V) buffer (last position zero): into ``grad`` when
+    given (as in :func:`cross_entropy`), else over the logits.  ``next_targets``:
+    ``input_ids`` is already the (B, S - 1) targets (the train loop's ``input_ids[:, 1:]``)."""
 
     device = _check_cuda(logits, input_ids)
-    b, s, bs, ss, v, ibs, iss = _shifted_desc(logits, input_ids)
-    if write_grad and not rows_disjoint([(b, bs), (s, ss)], v):
+    b, s, bs, ss, v, ibs, iss = _shifted_desc(logits, input_ids, next_targets)
+    gbs = gss = 0
+    if grad is not None:
+        if grad.shape != logits.shape or grad.dtype != logits.dtype or grad.device != logits.device:
+            raise ValueError("the gradient buffer must match the logits")
+        gbs, gss = grad.stride(0), grad.stride(1)
+        if grad.stride(2) != 1 and v > 1:
+            raise ValueError("the gradient buffer needs a contiguous vocabulary dimension")
+        if write_grad and not rows_disjoint([(b, gbs), (s, gss)], v):
+            raise ValueError("cross-entropy gradient rows overlap in memory")
+    elif write_grad and not rows_disjoint([(b, bs), (s, ss)], v):
         raise ValueError("cross-entropy logits rows overlap in memory; the gradient cannot be "
                          "written into them")
     ws_bytes = _lib.lib().pt_cross_entropy_workspace_bytes(b * s)
@@ -484,27 +547,34 @@ def cross_entropy_shifted(
     loss = torch.empty((), dtype=torch.float32, device=device)
     _lib.call(
         "pt_cross_entropy_shifted",
-        logits.data_ptr(), b, s, bs, ss, v, input_ids.data_ptr(), ibs, iss, int(ignore_index),
-        loss.data_ptr(), int(write_grad), ws.data_ptr(), ws_bytes, dtype_code(logits.dtype),
-        _stream(device),
+        logits.data_ptr(), b, s, bs, ss, v, _ids_ptr(input_ids, next_targets), ibs, iss,
+        int(ignore_index), loss.data_ptr(), int(write_grad), _ptr(grad), gbs, gss,
+        ws.data_ptr(), ws_bytes, dtype_code(logits.dtype), _stream(device),
     )
     return loss, ws
 
 
 def cross_entropy_shifted_scale_grad(
     dlogits: Tensor, input_ids: Tensor, grad_output: Tensor, ignore_index: int = -100,
-    workspace: Tensor | None = None,
+    workspace: Tensor | None = None, logits: Tensor | None = None, next_targets: bool = False,
 ) -> None:
     """dlogits *= grad_output in place for a gradient from :func:`cross_entropy_shifted`
-    (fp16: as :func:`cross_entropy_scale_grad`, with the forward's ``workspace``)."""
+    (fp16: as :func:`cross_entropy_scale_grad`, with the forward's ``workspace``, from
+    ``logits`` into ``dlogits`` when ``logits`` is given)."""
 
     device = _check_cuda(dlogits, input_ids, grad_output)
-    b, s, bs, ss, v, ibs, iss = _shifted_desc(dlogits, input_ids)
+    b, s, bs, ss, v, ibs, iss = _shifted_desc(dlogits, input_ids, next_targets)
+    lbs = lss = 0
+    if logits is not None:
+        if logits.shape != dlogits.shape or logits.dtype != dlogits.dtype:
+            raise ValueError("logits must match the gradient buffer")
+        lbs, lss = logits.stride(0), logits.stride(1)
     go = grad_output.detach().to(torch.float32).reshape(())
     _lib.call(
         "pt_cross_entropy_shifted_scale_grad",
-        dlogits.data_ptr(), b, s, bs, ss, v, input_ids.data_ptr(), ibs, iss, int(ignore_index),
-        go.data_ptr(), _ptr(workspace), dtype_code(dlogits.dtype), _stream(device),
+        dlogits.data_ptr(), b, s, bs, ss, v, _ids_ptr(input_ids, next_targets), ibs, iss,
+        int(ignore_index), go.data_ptr(), _ptr(logits), lbs, lss, _ptr(workspace),
+        dtype_code(dlogits.dtype), _stream(device),
     )
 
 

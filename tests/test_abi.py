@@ -74,12 +74,17 @@ def test_workspace_queries():
         ("pt_adamw_step", (ctypes.addressof(_HOST_TABLE), 2, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
         ("pt_grad_scale", (ctypes.addressof(_HOST_TABLE), 3, 2, None, None), _lib.PT_EINVAL),
         ("pt_copy", (None, None, 16, None), _lib.PT_EINVAL),
-        ("pt_cross_entropy", (None, 4, 1, 8, 0, 8, None, 1, 0, -100, None, 0, None, 0, 7, None), _lib.PT_EINVAL),
-        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EINVAL),
-        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 1 << 31, None, 3, 1, -100, None, 0, None, 0, 2, None), _lib.PT_EUNSUPPORTED),
-        ("pt_cross_entropy_shifted_scale_grad", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, None, 2, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy", (None, 4, 1, 8, 0, 8, None, 1, 0, -100, None, 0, None, 0, 0, None, 0, 7, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, 0, None, 0, 0, None, 0, 2, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_shifted", (None, 2, 3, 24, 8, 1 << 31, None, 3, 1, -100, None, 0, None, 0, 0, None, 0, 2, None), _lib.PT_EUNSUPPORTED),
+        ("pt_cross_entropy_shifted_scale_grad", (None, 2, 3, 24, 8, 8, None, 3, 1, -100, None, None, 0, 0, None, 2, None), _lib.PT_EINVAL),
         # fp16 needs the forward's workspace (n_valid): checked before anything is read
-        ("pt_cross_entropy_scale_grad", (16, 4, 1, 8, 0, 8, 16, 1, 0, -100, 16, None, 1, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_scale_grad", (16, 4, 1, 8, 0, 8, 16, 1, 0, -100, 16, None, 0, 0, None, 1, None), _lib.PT_EINVAL),
+        # a separate gradient whose rows start in another 16-byte phase than the logits rows
+        # (the addresses are never dereferenced: the check comes before any launch)
+        ("pt_cross_entropy", (4096, 4, 1, 8, 0, 8, 8192, 1, 0, -100, 12288, 1, 4098, 8, 0, 16384, 1 << 20, 2, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy", (4096, 4, 1, 8, 0, 8, 8192, 1, 0, -100, 12288, 1, 4096 + 64, 9, 0, 16384, 1 << 20, 2, None), _lib.PT_EINVAL),
+        ("pt_cross_entropy_shifted_scale_grad", (4096, 2, 3, 24, 8, 8, 8192, 3, 1, -100, 12288, 4100, 24, 8, 16384, 1, None), _lib.PT_EINVAL),
     ],
 )
 def test_invalid_arguments_rejected_before_launch(fn, args, code):
@@ -97,7 +102,7 @@ def test_empty_inputs_are_no_ops():
     assert lib.pt_swiglu_bwd(None, None, None, None, None, 5, 2, None) == _lib.PT_OK
     assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
     assert lib.pt_adamw_step_device_step(None, 0, 0, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None) == _lib.PT_OK
-    assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, None, 2, None) == _lib.PT_OK
+    assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, None, 0, 0, None, 2, None) == _lib.PT_OK
     assert lib.pt_last_error() == b""
 
 

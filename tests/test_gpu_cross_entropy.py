@@ -294,8 +294,8 @@ def _shifted_case(gpu, b, s, v, dtype, seed):
     return logits, ids
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("b,s,v", [(2, 65, 3000), (3, 17, 50257), (1, 9, 1001), (2, 2, 128)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,s,v", [(2, 65, 3000), (3, 17, 50257), (1, 9, 1001), (2, 2, 128), (2, 33, 32001)])
 def test_shifted_matches_the_train_loop_expression(gpu, dtype, b, s, v):
     logits, ids = _shifted_case(gpu, b, s, v, dtype, 7 * s + v)
     ref_loss, ref_grad = o_ce.shifted_forward_backward(logits, ids)
@@ -308,7 +308,15 @@ def test_shifted_matches_the_train_loop_expression(gpu, dtype, b, s, v):
     loss2, ws = ops.cross_entropy_shifted(buf, ids, write_grad=True)
     assert loss2.item() == loss.item()
     assert ops.cross_entropy_status(ws) == 0
-    _grad_close(buf, ref_grad, n_valid, dtype)
+    if dtype == torch.float16:
+        # the deferred gradient, written by the backward at a GradScaler-sized scale (odd
+        # vocabularies: the unaligned rows' head / body / tail split)
+        assert torch.equal(buf, logits)
+        scale = _fp16_scale_for(n_valid)
+        ops.cross_entropy_shifted_scale_grad(buf, ids, torch.full((), scale, device=gpu), workspace=ws)
+        _fp16_grad_close(buf, ref_grad, scale)
+    else:
+        _grad_close(buf, ref_grad, n_valid, dtype)
     assert bool((buf[:, -1, :] == 0).all())  # the last position has no target
 
 
@@ -531,3 +539,141 @@ def test_fp16_gradient_is_written_by_the_backward(gpu, vocab, offset, grad_outpu
     assert float(excess.max()) <= 0, float(excess.max())
     assert bool((logits[3] == 0).all())
     assert torch.equal(base[:, :offset], outside)
+
+
+# ------------------------------------------------------------------ gradient out of place
+
+
+def _graph_names(fn, depth=6):
+    names, frontier = [], [fn]
+    for _ in range(depth):
+        nxt = []
+        for f in frontier:
+            if f is None:
+                continue
+            names.append(type(f).__name__)
+            nxt.extend(n for n, _ in f.next_functions)
+        frontier = nxt
+    return names
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(
+    "rows,vocab,offset",
+    [(33, 8192, 0), (16, 50257, 0), (16, 50257, 1), (5, 131072, 0), (3, 151936, 0), (7, 1001, 3)],
+)
+def test_out_of_place_gradient_matches_in_place_bitwise(gpu, dtype, rows, vocab, offset):
+    # The gradient goes to a buffer of the logits' layout (same 16-byte phase row by row) and
+    # the logits are only read: the same bits as the in-place path on a copy of the logits in
+    # the same layout, the logits unchanged, and the oracle's values.
+    flat = randn((rows * vocab + offset,), dtype, gpu, rows + vocab + offset, 2.0)
+    logits = flat[offset:].view(rows, vocab)
+    g = torch.Generator(device=gpu).manual_seed(vocab + 1)
+    targets = torch.randint(0, vocab, (rows,), generator=g, device=gpu)
+    targets[1] = -100
+    before = logits.clone()
+    n_valid = rows - 1
+    ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
+    grad = ops.ce_grad_buffer(logits)
+    assert (grad.data_ptr() - logits.data_ptr()) % 16 == 0 and grad.stride() == logits.stride()
+    loss, ws = ops.cross_entropy(logits, targets, write_grad=True, grad=grad)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    assert ops.cross_entropy_status(ws) == 0
+    same = ops.ce_grad_buffer(logits)
+    same.copy_(before)
+    loss_ip, ws_ip = ops.cross_entropy(same, targets, write_grad=True)
+    assert loss_ip.item() == loss.item()
+    scale = _fp16_scale_for(n_valid) if dtype == torch.float16 else 0.37
+    go = torch.full((), scale, device=gpu)
+    if dtype == torch.float16:
+        assert torch.equal(logits, before)  # the forward wrote nothing
+        ops.cross_entropy_scale_grad(grad, targets, go, workspace=ws, logits=logits)
+        ops.cross_entropy_scale_grad(same, targets, go, workspace=ws_ip)
+        _fp16_grad_close(grad, ref_grad, scale)
+    else:
+        ops.cross_entropy_scale_grad(grad, targets, go, workspace=ws)
+        ops.cross_entropy_scale_grad(same, targets, go, workspace=ws_ip)
+        _grad_close(grad, scale * ref_grad, n_valid, dtype)
+    assert torch.equal(grad, same)
+    assert torch.equal(logits, before)
+
+
+def test_out_of_place_full_config_bf16(gpu):
+    rows, vocab = 8192, 128256
+    logits = randn((rows, vocab), torch.bfloat16, gpu, 51, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(52)
+    targets = torch.randint(0, vocab, (rows,), generator=g, device=gpu)
+    targets[torch.randperm(rows, generator=g, device=gpu)[:410]] = -100
+    ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
+    digest_before = logits.view(torch.int16).sum(dtype=torch.int64).item()
+    grad = ops.ce_grad_buffer(logits)
+    loss, ws = ops.cross_entropy(logits, targets, write_grad=True, grad=grad)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    _grad_close(grad, ref_grad, rows - 410, torch.bfloat16)
+    assert logits.view(torch.int16).sum(dtype=torch.int64).item() == digest_before
+    del ref_grad
+    ref_loss2, _ = o_ce.forward_backward(logits[:64], targets[:64])  # the logits are still the logits
+    loss2, _ = ops.cross_entropy(logits[:64], targets[:64])
+    assert abs(loss2.item() - ref_loss2.item()) <= LOSS_RTOL * abs(ref_loss2.item())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,s,v", [(2, 65, 3000), (3, 17, 50257), (1, 9, 1001), (2, 2, 128)])
+def test_reference_call_site_unchanged(gpu, dtype, b, s, v):
+    # The train loop's own call, CrossEntropyWithFallback(...)(logits[:, :-1, :].transpose(1, 2),
+    # input_ids[:, 1:]) with the default inplace=False, is computed on the view's base: the
+    # logits stay untouched, the graph holds no slice or transpose backward, and the base's
+    # gradient (last position zero) matches the oracle.
+    import warnings
+
+    from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback
+
+    full, ids = _shifted_case(gpu, b, s, v, dtype, 11 * s + v)
+    n_valid = int((ids[:, 1:] != -100).sum())
+    ref_loss, ref_grad = o_ce.shifted_forward_backward(full, ids)
+    leaf = full.clone().requires_grad_(True)
+    logits = leaf * 1  # non-leaf, as the language-model head's output
+    before = logits.detach().clone()
+    ce = CrossEntropyWithFallback(use_triton=True)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        loss = ce(logits[:, :-1, :].transpose(1, 2), ids[:, 1:])
+    names = _graph_names(loss.grad_fn)
+    assert not any("Slice" in n or "Transpose" in n for n in names), names
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    scale = _fp16_scale_for(n_valid) if dtype == torch.float16 else 2.5
+    (scale * loss).backward()
+    assert torch.equal(logits.detach(), before)
+    if dtype == torch.float16:
+        _fp16_grad_close(leaf.grad, ref_grad, scale)
+    else:
+        _grad_close(leaf.grad, scale * ref_grad, n_valid, dtype)
+    assert bool((leaf.grad[:, -1, :] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_other_views_take_the_generic_out_of_place_path(gpu, dtype):
+    # logits[:, 1:, :].transpose(1, 2) is not the train loop's view: the loss runs on the view
+    # itself, its gradient goes to a buffer of the view's layout, and autograd's slice
+    # backward places it; the logits stay untouched.
+    from picotron_amd.nn.triton_kernels import triton_cross_entropy
+
+    full, ids = _shifted_case(gpu, 2, 40, 1001, dtype, 97)
+    view_ref = full[:, 1:, :].transpose(1, 2)
+    targets = ids[:, :-1]
+    ref_loss, ref_grad = o_ce.forward_backward(view_ref, targets)
+    n_valid = int((targets != -100).sum())
+    leaf = full.clone().requires_grad_(True)
+    logits = leaf * 1
+    before = logits.detach().clone()
+    loss = triton_cross_entropy(logits[:, 1:, :].transpose(1, 2), targets, inplace=False)
+    assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
+    scale = _fp16_scale_for(n_valid) if dtype == torch.float16 else 1.0
+    (scale * loss).backward()
+    assert torch.equal(logits.detach(), before)
+    expected = torch.zeros(full.shape, dtype=torch.float64, device=gpu)
+    expected[:, 1:, :] = ref_grad.to(gpu).transpose(1, 2)
+    if dtype == torch.float16:
+        _fp16_grad_close(leaf.grad, expected, scale)
+    else:
+        _grad_close(leaf.grad, expected, n_valid, dtype)

@@ -246,10 +246,12 @@ def test_fp16_grad_scaler_training_steps_track_the_fallback_loop(gpu):
         assert abs(losses[0] - losses[1]) <= 5e-3 * abs(losses[1]), (step, losses)
     for (name, p_f), p_r in zip(fused.named_parameters(), reference.parameters()):
         assert bool(torch.isfinite(p_f).all()), name
-        # three Adam updates of at most lr each: the runs may differ only where a gradient's
-        # sign is within its fp16 rounding, so by far most elements agree closely
+        # three Adam updates of about lr each: the runs may differ by up to a few lr only where
+        # a gradient's sign is within its fp16 rounding (measured on MI355X: at most 0.2 % of
+        # a tensor's elements beyond 0.1 lr, mean difference at most 0.0017 lr per tensor), so
+        # both bounds sit about 5x above what was measured
         diff = (p_f.detach() - p_r.detach()).abs()
-        assert float(diff.max()) <= 6.01 * hp["lr"], name
-        assert float((diff > 0.1 * hp["lr"]).float().mean()) < 0.02, name
+        assert float(diff.mean()) <= 0.01 * hp["lr"], name
+        assert float((diff > 0.1 * hp["lr"]).float().mean()) < 0.01, name
     # growth_interval 2 over three clean steps: the scale doubled once
     assert runs[0]["scaler"].get_scale() == 2.0 ** 13

@@ -175,18 +175,31 @@ def test_shifted_cross_entropy_random(gpu, case):
     b = int(rng.integers(1, 4))
     s = _log_uniform(rng, 2, 300)
     v = _log_uniform(rng, 2, 150_000)
-    dtype = [torch.float32, torch.bfloat16][rng.integers(2)]
-    print(f"shifted cross-entropy case {case}: b {b} s {s} v {v} {dtype}", flush=True)
+    dtype = DTYPES[rng.integers(3)]
+    out_of_place = bool(rng.integers(2))
+    print(f"shifted cross-entropy case {case}: b {b} s {s} v {v} {dtype} "
+          f"{'out of place' if out_of_place else 'in place'}", flush=True)
     logits, ids = t_ce._shifted_case(gpu, b, s, v, dtype, 6000 + case)
     if not bool((ids[:, 1:] != -100).any()):
         ids[0, 1] = 0
     ref_loss, ref_grad = t_ce.o_ce.shifted_forward_backward(logits, ids)
     n_valid = int((ids[:, 1:] != -100).sum())
-    buf = logits.clone()
-    loss, ws = ops.cross_entropy_shifted(buf, ids, write_grad=True)
+    before = logits.clone()
+    buf = ops.ce_grad_buffer(logits, 2) if out_of_place else logits.clone()
+    src = logits if out_of_place else buf
+    loss, ws = ops.cross_entropy_shifted(src, ids, write_grad=True,
+                                         grad=buf if out_of_place else None)
     assert abs(loss.item() - ref_loss.item()) <= t_ce.LOSS_RTOL * abs(ref_loss.item())
     assert ops.cross_entropy_status(ws) == 0
-    t_ce._grad_close(buf, ref_grad, n_valid, dtype)
+    if dtype == torch.float16:
+        # the deferred gradient at a GradScaler-sized scale (as in the module's _check)
+        scale = t_ce._fp16_scale_for(n_valid)
+        ops.cross_entropy_shifted_scale_grad(buf, ids, torch.full((), scale, device=gpu), workspace=ws,
+                                             logits=logits if out_of_place else None)
+        t_ce._fp16_grad_close(buf, ref_grad, scale)
+    else:
+        t_ce._grad_close(buf, ref_grad, n_valid, dtype)
+    assert torch.equal(logits, before)
 
 
 @pytest.mark.parametrize("case", range(CASES // 2))
