@@ -106,6 +106,42 @@ __device__ __forceinline__ float block_reduce_sum(float v, float* red) {
   return t;
 }
 
+// Loads per thread that the one-block kernels (ce_prepare, ce_finish) keep in flight together.
+constexpr int kFinishBatch = 8;
+
+// This thread's count of kept targets among rows tid, tid + kThreads, ...: kFinishBatch
+// targets in flight together (a load under a branch would be waited for before the next is
+// issued: one round trip each); a row without a target loads targets[0] and is not counted.
+template <bool SMALL>
+__device__ __forceinline__ float count_kept_batched(const int64_t* __restrict__ targets,
+                                                    int64_t inner, int64_t valid_inner,
+                                                    int64_t tos, int64_t tis, int64_t rows,
+                                                    int64_t ignore_index) {
+  float cnt = 0.0f;
+  for (int64_t base = threadIdx.x; base < rows; base += int64_t{kThreads} * kFinishBatch) {
+    int64_t t[kFinishBatch];
+    bool kept[kFinishBatch];
+#pragma unroll
+    for (int u = 0; u < kFinishBatch; ++u) {
+      const int64_t r = base + static_cast<int64_t>(u) * kThreads;
+      int64_t o, i;
+      if constexpr (SMALL) {
+        const uint32_t o32 = static_cast<uint32_t>(r) / static_cast<uint32_t>(inner);
+        o = o32;
+        i = static_cast<uint32_t>(r) - o32 * static_cast<uint32_t>(inner);
+      } else {
+        o = r / inner;
+        i = r - o * inner;
+      }
+      kept[u] = r < rows && i < valid_inner;
+      t[u] = targets[kept[u] ? o * tos + i * tis : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < kFinishBatch; ++u) cnt += (kept[u] && t[u] != ignore_index) ? 1.0f : 0.0f;
+  }
+  return cnt;
+}
+
 __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __restrict__ targets,
                                                                int64_t inner, int64_t valid_inner,
                                                                int64_t tos, int64_t tis,
@@ -114,9 +150,14 @@ __global__ __launch_bounds__(kThreads) void ce_prepare_kernel(const int64_t* __r
                                                                float* __restrict__ loss_out) {
   __shared__ float red[kWaves];
   float cnt = 0.0f;
-  for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
-    const int64_t o = r / inner, i = r - (r / inner) * inner;
-    if (i < valid_inner) cnt += (targets[o * tos + i * tis] != ignore_index) ? 1.0f : 0.0f;
+  // Row decode in 32 bits when the counts allow it (the 64-bit division is a long
+  // instruction sequence per target).
+  if (valid_inner > 0) {
+    if (rows + int64_t{kThreads} * kFinishBatch <= 0xffffffffLL) {
+      cnt = count_kept_batched<true>(targets, inner, valid_inner, tos, tis, rows, ignore_index);
+    } else {
+      cnt = count_kept_batched<false>(targets, inner, valid_inner, tos, tis, rows, ignore_index);
+    }
   }
   const float total = block_reduce_sum(cnt, red);
   if (threadIdx.x == 0) {
@@ -751,7 +792,19 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
   __shared__ float red[kWaves];
   const float* rl = row_losses(ws);
   float acc = 0.0f;
-  for (int64_t r = threadIdx.x; r < rows; r += kThreads) acc += rl[r];
+  // kFinishBatch losses per thread in flight together, added in increasing row order (the
+  // order of one load at a time); rows past the end load the last row's loss and add 0.
+  for (int64_t base = threadIdx.x; base < rows; base += int64_t{kThreads} * kFinishBatch) {
+    float v[kFinishBatch];
+#pragma unroll
+    for (int u = 0; u < kFinishBatch; ++u) {
+      const int64_t r = base + static_cast<int64_t>(u) * kThreads;
+      v[u] = rl[r < rows ? r : rows - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kFinishBatch; ++u)
+      acc += base + static_cast<int64_t>(u) * kThreads < rows ? v[u] : 0.0f;
+  }
   const float total = block_reduce_sum(acc, red);
   if (threadIdx.x == 0) *loss_out = total / ws->n_valid;
 }
