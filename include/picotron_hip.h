@@ -87,7 +87,9 @@ int pt_rmsnorm_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t
  * pt_rmsnorm_bwd (bitwise: same kernels and grid).  Returns PT_EUNSUPPORTED when the
  * partials, pt_rmsnorm_bwd_workspace_bytes(rows, cols, x_dtype), exceed 16 MiB (e.g. more
  * than 8192 columns at 16384 rows).  Calls that overlap on one device share the array and
- * race: issue them on one stream, or serialise them. */
+ * race: issue them on one stream, or serialise them.  The first call on a device looks up
+ * the array's device address and must not be made inside a graph capture (it returns
+ * PT_EUNSUPPORTED there); later calls can be captured and replayed. */
 int pt_rmsnorm_bwd_noalloc(const void* dy, int64_t dy_row_stride, const void* x,
                            int64_t x_row_stride, const void* weight, const float* rstd, void* dx,
                            int64_t dx_row_stride, void* dweight, int64_t rows, int64_t cols,
