@@ -405,19 +405,21 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
       out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(v[k].e[i]) * f);
     }
     // One add per store rather than sixteen offsets held in registers across the row.
+    // Gradient stores write through L2 (as the RMSNorm forward's do): a [8192, 128256] bf16
+    // call measured 1-6 µs faster than with nontemporal stores alone, never slower.
     int vo = voff + k * kChunkBytes;
     asm volatile("" : "+v"(vo));
-    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kWriteThrough);
   }
   if (!bad && tid == owner) {
     Vec16<T> one;
     one.e[0] = Elem<T>::from_f32(target_grad(M, S, xt, inv_n_of(ws)));
     const int toff = static_cast<int>(cur.tgt) * static_cast<int>(sizeof(T));
     if constexpr (sizeof(T) == 4) {
-      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kWriteThrough);
     } else {
       __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
-                                            gbuf, toff, 0, kNonTemporal);
+                                            gbuf, toff, 0, kWriteThrough);
     }
   }
 }
@@ -669,7 +671,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     for (int i = 0; i < V; ++i) out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(kv[k].e[i]) * f);
     int vo = voff + k * kChunkBytes;
     asm volatile("" : "+v"(vo));
-    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kNonTemporal);
+    __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kWriteThrough);
   }
   for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
@@ -684,7 +686,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
       for (int i = 0; i < V; ++i)
         out.e[i] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(v[u].e[i]), M) * scale);
       __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, voff + b + u * kChunkBytes, 0,
-                                             kNonTemporal);
+                                             kWriteThrough);
     }
   }
   if (my_edge >= 0) g[my_edge] = Elem<T>::from_f32(exp_shifted(Elem<T>::to_f32(p[my_edge]), M) * scale);
@@ -703,10 +705,10 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
         one.e[0] = gt;
         const int toff = (t - head) * static_cast<int>(sizeof(T));
         if constexpr (sizeof(T) == 4) {
-          __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kNonTemporal);
+          __builtin_amdgcn_raw_buffer_store_b32(one.raw[0], gbuf, toff, 0, kWriteThrough);
         } else {
           __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(one.raw[0] & 0xffffu),
-                                                gbuf, toff, 0, kNonTemporal);
+                                                gbuf, toff, 0, kWriteThrough);
         }
       } else {
         g[t] = gt;
@@ -928,7 +930,7 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* logits, const T* src, 
     }
 #pragma unroll
     for (int k = 0; k < kScaleVecs; ++k)
-      __builtin_amdgcn_raw_buffer_store_b128(out[k].raw, sbuf, (k * 256 + tid) * 16, 0, kNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(out[k].raw, sbuf, (k * 256 + tid) * 16, 0, kWriteThrough);
     if constexpr (!ALIGNED) {
       if (c == 0) {
         // The value is rounded to fp32 before the conversion, as in the vector path (left
