@@ -510,7 +510,8 @@ class HeadlineWorkload(Workload):
                 "tokens_per_s": round(wl.tokens_per_step / sec, 1),
             }
         ops_out["rmsnorm"].update(self.rms.extra(steps))
-        return {"ops": ops_out, "other_configs": _other_configs(steps)}
+        return {"ops": ops_out, "other_configs": _other_configs(steps),
+                "quickstart_step": _quickstart_line(steps=200)}
 
     def cpu_baseline(self) -> dict:
         rms, swiglu = self.rms.cpu_baseline(), self.swiglu.cpu_baseline()
@@ -1563,6 +1564,202 @@ class CopyWorkload(Workload):
         return None
 
 
+# ------------------------------------------------------------------ quickstart training step
+
+# The reference's quickstart model and batch (src/picotron/config/picotron_decoder.yaml:7-10,
+# 16-19): vocabulary 64, hidden 32, intermediate 64, 2 layers, 4 heads, sequence 16, micro-batch 2,
+# learning rate 1e-3; AdamW betas (0.9, 0.999), eps 1e-8, weight decay 0 and no clipping are the
+# config defaults (src/picotron/config/config.py:360-366,384-385).
+QUICKSTART = dict(vocab=64, hidden=32, intermediate=64, layers=2, heads=4, seq=16, batch=2, lr=1e-3)
+QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused")
+
+
+class _QuickstartBlock(torch.nn.Module):
+    """The reference's decoder block (src/picotron/models/picotron_decoder.py:70-130): attention
+    norm, causal self-attention (src/picotron/nn/attention.py: bias-free q/k/v/o projections,
+    heads split to (B, H, S, D), RoPE on q and k, SDPA under a boolean causal mask), residual add,
+    MLP norm, SwiGLU MLP, residual add.  The attention product runs in fp32 in every variant
+    (plain PyTorch, identical between them)."""
+
+    def __init__(self, fused: bool) -> None:
+        from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU
+
+        super().__init__()
+        h, heads = QUICKSTART["hidden"], QUICKSTART["heads"]
+        self.heads, self.head_dim = heads, h // heads
+        self.attention_norm = RMSNorm(h, use_triton_rmsnorm=fused)
+        self.query_projection = torch.nn.Linear(h, h, bias=False)
+        self.key_projection = torch.nn.Linear(h, h, bias=False)
+        self.value_projection = torch.nn.Linear(h, h, bias=False)
+        self.output_projection = torch.nn.Linear(h, h, bias=False)
+        self.rotary_embedding = RotaryEmbedding(self.head_dim, 10_000.0, use_triton_rope=fused)
+        self.mlp_norm = RMSNorm(h, use_triton_rmsnorm=fused)
+        self.mlp = SwiGLU(h, QUICKSTART["intermediate"], use_triton_swiglu=fused)
+
+    def _attention(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, h = x.shape
+        split = lambda t: t.view(b, s, self.heads, self.head_dim).transpose(1, 2)  # noqa: E731
+        q, k = self.rotary_embedding(split(self.query_projection(x)), split(self.key_projection(x)))
+        v = split(self.value_projection(x))
+        positions = torch.arange(s, device=x.device)
+        mask = positions.unsqueeze(0) <= positions.unsqueeze(1)
+        out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask,
+                                             scale=self.head_dim ** -0.5)
+        return self.output_projection(out.to(q.dtype).transpose(1, 2).reshape(b, s, h))
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        hidden = hidden + self._attention(self.attention_norm(hidden))
+        return hidden + self.mlp(self.mlp_norm(hidden))
+
+
+class _QuickstartDecoder(torch.nn.Module):
+    """The reference's decoder (src/picotron/models/picotron_decoder.py:133-220) with RoPE
+    positions and an untied output projection, built from this package's modules; ``fused``
+    sets every module's kernel flag, as ``model.triton_kernels`` does."""
+
+    def __init__(self, fused: bool) -> None:
+        from picotron_amd.nn import RMSNorm
+
+        super().__init__()
+        v, h = QUICKSTART["vocab"], QUICKSTART["hidden"]
+        self.token_embeddings = torch.nn.Embedding(v, h)
+        self.layers = torch.nn.ModuleList(_QuickstartBlock(fused) for _ in range(QUICKSTART["layers"]))
+        self.final_norm = RMSNorm(h, use_triton_rmsnorm=fused)
+        self.output_projection = torch.nn.Linear(h, v, bias=False)
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        hidden = self.token_embeddings(input_ids)
+        for layer in self.layers:
+            hidden = layer(hidden)
+        return self.output_projection(self.final_norm(hidden))
+
+
+class QuickstartTrainer:
+    """One training step of the quickstart model as the train loop runs it
+    (src/picotron/training/train_loop.py:134-168, the plain AdamW branch): zero_grad, forward and
+    the next-token loss on the (B, V, S-1) logits view under bf16 autocast (what ``dtype: auto``
+    resolves to on a bf16 GPU, train_loop.py:57,274-282), backward, optimizer step.
+
+    ``variant``: ``eager_reference`` runs the modules with their kernel flags off, torch's loss
+    and torch's AdamW step (the reference's fallbacks); ``eager_fused`` the same model with every
+    flag on, ``CrossEntropyWithFallback(use_triton=True)`` and ``AdamWStepWithFallback``;
+    the ``graph_*`` variants capture that whole step in one HIP graph (capturable AdamW,
+    gradients zeroed in place so that their addresses stay fixed) and replay it.  ``capturable``
+    overrides the optimizer's flag (by default set for the graph variants only)."""
+
+    def __init__(self, variant: str, seed: int = 1337, capturable: bool | None = None) -> None:
+        from picotron_amd.nn.triton_kernels import AdamWStepWithFallback, CrossEntropyWithFallback
+
+        if variant not in QUICKSTART_VARIANTS:
+            raise ValueError(f"unknown variant {variant}")
+        self.variant = variant
+        fused = variant.endswith("fused")
+        self.graphed = variant.startswith("graph")
+        torch.manual_seed(seed)
+        self.model = _QuickstartDecoder(fused).cuda()
+        self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=QUICKSTART["lr"], betas=(0.9, 0.999),
+                                           eps=1e-8, weight_decay=0.0,
+                                           capturable=self.graphed if capturable is None else capturable)
+        self.loss_function = CrossEntropyWithFallback(use_triton=fused)
+        self.optimizer_step = AdamWStepWithFallback(use_triton=fused)
+        self.graph = None
+        self.static_ids = None
+
+    def _step(self, input_ids: torch.Tensor) -> torch.Tensor:
+        self.optimizer.zero_grad(set_to_none=not self.graphed)
+        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=not self.graphed):
+            logits = self.model(input_ids)
+            loss = self.loss_function(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:])
+        loss.backward()
+        self.optimizer_step.step(self.optimizer)
+        return loss.detach()
+
+    def prepare(self, input_ids: torch.Tensor, warmup: int = 3) -> None:
+        """Warm-up steps (optimizer state, cached tables), then the capture for a graph
+        variant.  Fails if a fused module fell back to PyTorch."""
+
+        import warnings
+
+        with warnings.catch_warnings(record=True) as caught:
+            warnings.simplefilter("always")
+            if self.graphed:
+                self.static_ids = input_ids.clone()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    for _ in range(warmup):
+                        self._step(self.static_ids)
+                torch.cuda.current_stream().wait_stream(side)
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph):
+                    self.static_loss = self._step(self.static_ids)
+            else:
+                for _ in range(warmup):
+                    self._step(input_ids)
+            torch.cuda.synchronize()
+        fallbacks = [str(w.message) for w in caught if "unavailable" in str(w.message)]
+        if fallbacks:
+            raise RuntimeError(f"{self.variant}: a fused kernel fell back to PyTorch: {fallbacks[0]}")
+
+    def step(self, input_ids: torch.Tensor) -> torch.Tensor:
+        if self.graph is None:
+            return self._step(input_ids)
+        self.static_ids.copy_(input_ids)
+        self.graph.replay()
+        return self.static_loss
+
+
+def _quickstart_line(steps: int) -> dict:
+    """The quickstart step figures with what they describe (a section of the default line)."""
+
+    q = QUICKSTART
+    return {
+        "workload": (f"one training step of the quickstart decoder (vocab {q['vocab']}, hidden {q['hidden']}, "
+                     f"intermediate {q['intermediate']}, {q['layers']} layers, {q['heads']} heads), micro-batch "
+                     f"{q['batch']} x sequence {q['seq']}, bf16 autocast: zero_grad, forward, next-token loss on "
+                     f"the (B, V, S-1) view, backward, AdamW step; batches resident on the device"),
+        "steps": steps,
+        "variants": quickstart_step_figures(steps),
+    }
+
+
+def quickstart_step_figures(steps: int = 200, variants=QUICKSTART_VARIANTS) -> dict:
+    """Per variant: the host time to issue one step, the wall time per step when steps are
+    issued back to back (the slower of host and device sets it), the device time per step
+    between HIP events around those steps, and the wall time per step in the train loop's own
+    form, which reads the loss back after every step (train_loop.py:169)."""
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    batches = torch.randint(0, QUICKSTART["vocab"], (steps, QUICKSTART["batch"], QUICKSTART["seq"]),
+                            generator=g, device="cuda")
+    out = {}
+    for variant in variants:
+        trainer = QuickstartTrainer(variant)
+        trainer.prepare(batches[0])
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(steps):
+            trainer.step(batches[i])
+        end.record()
+        issued = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for i in range(steps):
+            trainer.step(batches[i]).item()
+        loop = time.perf_counter() - t0
+        out[variant] = {
+            "host_issue_us_per_step": round(issued / steps * 1e6, 1),
+            "wall_us_per_step": round(wall / steps * 1e6, 1),
+            "device_us_per_step": round(start.elapsed_time(end) / steps * 1e3, 1),
+            "train_loop_us_per_step": round(loop / steps * 1e6, 1),
+        }
+        del trainer
+    return out
+
+
 WORKLOADS = {
     "headline": HeadlineWorkload,
     "rmsnorm": RMSNormWorkload,
@@ -1697,12 +1894,47 @@ def _cpu_line(wl: Workload) -> dict | None:
     return cpu
 
 
+def _quickstart_main(args) -> int:
+    """The quickstart training step as its own line: value = tokens per second of the
+    graph-captured fused step (or of the one variant asked for), steps issued back to back."""
+
+    variants = QUICKSTART_VARIANTS if args.variant == "all" else (args.variant,)
+    line = _quickstart_line(args.steps) if args.variant == "all" else {
+        "steps": args.steps, "variants": quickstart_step_figures(args.steps, variants)}
+    figs = line["variants"]
+    lead = "graph_fused" if "graph_fused" in figs else variants[0]
+    us = figs[lead]["wall_us_per_step"]
+    tokens = QUICKSTART["batch"] * QUICKSTART["seq"]
+    result = {
+        "metric": f"quickstart decoder training step ({lead}), tokens/s",
+        "value": round(tokens / (us * 1e-6), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": 3,
+        "ms_per_step": round(us * 1e-3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic token ids (seeded on device)",
+        "config": {"tokens_per_step": tokens, "parallelism": "single GPU", **line},
+        # a few microseconds of work per kernel: launch latency, not HBM, bounds this step
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description="fused-kernel HBM benchmark (one MI355X)")
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
+    parser.add_argument("--workload", choices=sorted([*WORKLOADS, "quickstart_step"]), default="headline")
+    parser.add_argument("--variant", choices=("all", *QUICKSTART_VARIANTS), default="all",
+                        help="quickstart_step only: the step variant(s) to time")
     parser.add_argument("--layers", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra", action="store_true",
@@ -1723,6 +1955,8 @@ def main() -> int:
         print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)
         return 2
 
+    if args.workload == "quickstart_step":
+        return _quickstart_main(args)
     global _WITH_CPU_BASELINE
     _WITH_CPU_BASELINE = not args.no_cpu_baseline
     layers = args.layers or DEFAULT_LAYERS[args.workload]
