@@ -1571,7 +1571,8 @@ class CopyWorkload(Workload):
 # learning rate 1e-3; AdamW betas (0.9, 0.999), eps 1e-8, weight decay 0 and no clipping are the
 # config defaults (src/picotron/config/config.py:360-366,384-385).
 QUICKSTART = dict(vocab=64, hidden=32, intermediate=64, layers=2, heads=4, seq=16, batch=2, lr=1e-3)
-QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused")
+QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused",
+                       "graph_fused_residual")
 
 
 class _QuickstartBlock(torch.nn.Module):
@@ -1611,16 +1612,27 @@ class _QuickstartBlock(torch.nn.Module):
         hidden = hidden + self._attention(self.attention_norm(hidden))
         return hidden + self.mlp(self.mlp_norm(hidden))
 
+    def forward_residual(self, hidden: torch.Tensor, normed: torch.Tensor, next_norm) -> tuple:
+        """The same block with each residual add fused into the norm after it
+        (``RMSNorm.add_and_norm``): takes the residual stream and this block's normed input,
+        returns the stream and ``next_norm`` of it.  The autocast branch outputs are promoted
+        to the stream's fp32 first, as the plain ``+`` promotes them."""
+
+        attn = self._attention(normed).to(hidden.dtype)
+        hidden, normed = self.mlp_norm.add_and_norm(attn, hidden)
+        return next_norm.add_and_norm(self.mlp(normed).to(hidden.dtype), hidden)
+
 
 class _QuickstartDecoder(torch.nn.Module):
     """The reference's decoder (src/picotron/models/picotron_decoder.py:133-220) with RoPE
     positions and an untied output projection, built from this package's modules; ``fused``
     sets every module's kernel flag, as ``model.triton_kernels`` does."""
 
-    def __init__(self, fused: bool) -> None:
+    def __init__(self, fused: bool, residual: bool = False) -> None:
         from picotron_amd.nn import RMSNorm
 
         super().__init__()
+        self.residual = residual
         v, h = QUICKSTART["vocab"], QUICKSTART["hidden"]
         self.token_embeddings = torch.nn.Embedding(v, h)
         self.layers = torch.nn.ModuleList(_QuickstartBlock(fused) for _ in range(QUICKSTART["layers"]))
@@ -1629,6 +1641,12 @@ class _QuickstartDecoder(torch.nn.Module):
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         hidden = self.token_embeddings(input_ids)
+        if self.residual:
+            normed = self.layers[0].attention_norm(hidden)
+            norms = [layer.attention_norm for layer in self.layers[1:]] + [self.final_norm]
+            for layer, next_norm in zip(self.layers, norms):
+                hidden, normed = layer.forward_residual(hidden, normed, next_norm)
+            return self.output_projection(normed)
         for layer in self.layers:
             hidden = layer(hidden)
         return self.output_projection(self.final_norm(hidden))
@@ -1644,7 +1662,9 @@ class QuickstartTrainer:
     and torch's AdamW step (the reference's fallbacks); ``eager_fused`` the same model with every
     flag on, ``CrossEntropyWithFallback(use_triton=True)`` and ``AdamWStepWithFallback``;
     the ``graph_*`` variants capture that whole step in one HIP graph (capturable AdamW,
-    gradients zeroed in place so that their addresses stay fixed) and replay it.  ``capturable``
+    gradients zeroed in place so that their addresses stay fixed) and replay it.
+    ``graph_fused_residual`` also fuses each residual add into the norm after it
+    (``RMSNorm.add_and_norm``), a change to the model's code rather than a flag.  ``capturable``
     overrides the optimizer's flag (by default set for the graph variants only)."""
 
     def __init__(self, variant: str, seed: int = 1337, capturable: bool | None = None) -> None:
@@ -1653,10 +1673,10 @@ class QuickstartTrainer:
         if variant not in QUICKSTART_VARIANTS:
             raise ValueError(f"unknown variant {variant}")
         self.variant = variant
-        fused = variant.endswith("fused")
+        fused = "fused" in variant
         self.graphed = variant.startswith("graph")
         torch.manual_seed(seed)
-        self.model = _QuickstartDecoder(fused).cuda()
+        self.model = _QuickstartDecoder(fused, residual=variant.endswith("residual")).cuda()
         self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=QUICKSTART["lr"], betas=(0.9, 0.999),
                                            eps=1e-8, weight_decay=0.0,
                                            capturable=self.graphed if capturable is None else capturable)

@@ -34,3 +34,20 @@ def test_graph_replays_match_eager_steps(gpu, kind):
     for (name, a), b in zip(graphed.model.named_parameters(), eager.model.parameters()):
         torch.testing.assert_close(a.detach(), b.detach(), rtol=1e-5, atol=1e-6, msg=name)
 
+
+
+def test_residual_fused_model_takes_the_same_steps(gpu):
+    """The model with each residual add fused into the norm after it computes the same steps
+    as the plain model (the adds are the same fp32 adds; the norms may round differently)."""
+
+    batches = _batches(6)
+    plain, fused = QuickstartTrainer("graph_fused"), QuickstartTrainer("graph_fused_residual")
+    plain.prepare(batches[0])
+    fused.prepare(batches[0])
+    for i in range(1, 6):
+        loss_p = plain.step(batches[i]).clone()
+        loss_f = fused.step(batches[i])
+        torch.cuda.synchronize()
+        torch.testing.assert_close(loss_f, loss_p, rtol=1e-4, atol=1e-5, msg=f"step {i}")
+    for (name, a), b in zip(fused.model.named_parameters(), plain.model.parameters()):
+        torch.testing.assert_close(a.detach(), b.detach(), rtol=1e-4, atol=1e-5, msg=name)
