@@ -43,7 +43,7 @@ int validate(const char* fn, int64_t rows, int64_t cols, int xdt, int wdt, bool 
   if (rows > (int64_t{1} << 36)) return fail(PT_EUNSUPPORTED, std::string(fn) + ": rows too large");
   const int vec = 16 / dtype_size(xdt);
   const int cap = cap_of(backward ? bwd_vpl_cap_for(tuning().bwd_vpl_cap, cols, vec)
-                                  : tuning().fwd_vpl_cap);
+                                  : fwd_vpl_cap_for(tuning().fwd_vpl_cap, vec));
   if (!choose_shape(cols, vec, cap, s))
     return fail(PT_EUNSUPPORTED, std::string(fn) + ": hidden size " + std::to_string(cols) +
                                      " exceeds the register-resident row capacity (" +

@@ -620,7 +620,7 @@ struct Shape {
 // per process.  The backward partial count fixes the
 // weight-gradient summation order, so dW is reproducible for a given setting.
 struct Tuning {
-  int fwd_vpl_cap = 4;
+  int fwd_vpl_cap = 0;  // 0: by element size (fwd_vpl_cap_for)
   int bwd_vpl_cap = 0;  // 0: by row length (bwd_vpl_cap_for)
   int64_t fwd_blocks_per_cu = 0;  // 0: no cap (one row per row slot)
   int64_t bwd_partials = 512;
@@ -635,6 +635,12 @@ inline int bwd_vpl_cap_for(int tuned, int64_t cols, int vec) {
   if (tuned > 0) return tuned;
   return (cols + vec - 1) / vec <= 256 ? 1 : 2;
 }
+
+// Forward vectors per lane: 32 elements per lane, four 16-byte vectors of a 16-bit type and
+// eight of fp32 (two waves per 4096-wide row either way); measured at [16384, 4096], 4 layers:
+// bf16 0.4628-0.4639 ms per step against 0.4660-0.4684 with two and 0.4747-0.4763 with eight,
+// fp32 0.8769-0.8777 ms against 0.8868-0.8871 with four.
+inline int fwd_vpl_cap_for(int tuned, int vec) { return tuned > 0 ? tuned : 32 / vec; }
 
 inline int64_t env_positive(const char* name, int64_t fallback) {
   const char* v = std::getenv(name);
