@@ -511,8 +511,12 @@ class HeadlineWorkload(Workload):
             }
         ops_out["rmsnorm"].update(self.rms.extra(steps))
         # before the other configurations, whose CPU baselines leave the host cores busy
-        # for a while, which slows the host-bound eager steps
-        quickstart = _quickstart_line(steps=200)
+        # for a while, which slows the host-bound eager steps; a failure here (it runs torch's
+        # own kernels and graph capture too) is reported in the line rather than ending it
+        try:
+            quickstart = _quickstart_line(steps=200)
+        except Exception as error:  # noqa: BLE001
+            quickstart = {"error": f"{type(error).__name__}: {error}"}
         return {"ops": ops_out, "other_configs": _other_configs(steps), "quickstart_step": quickstart}
 
     def cpu_baseline(self) -> dict:
