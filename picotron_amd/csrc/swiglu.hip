@@ -57,13 +57,18 @@ __global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ g
   }
 }
 
-template <typename T, int UNROLL, bool NT>
+// WT: the two gradients are stored through buffer resources with the write-through policy
+// (host-checked: every byte offset fits 31 bits) instead of nontemporal global stores.
+template <typename T, int UNROLL, bool NT, bool WT>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ dy,
                                                          const T* __restrict__ g,
                                                          const T* __restrict__ u,
                                                          T* __restrict__ dg, T* __restrict__ du,
                                                          int64_t nvec) {
   constexpr int V = Elem<T>::VEC;
+  const int bytes = WT ? static_cast<int>(nvec * 16) : 0;
+  const auto gbuf = uniform_buffer(dg, dg != nullptr ? bytes : 0);
+  const auto ubuf = uniform_buffer(du, du != nullptr ? bytes : 0);
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * UNROLL;
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * UNROLL + threadIdx.x; base < nvec;
        base += stride) {
@@ -91,8 +96,14 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ d
           gov.e[j] = Elem<T>::from_f32((d * uf) * (s * (1.0f + gf * (1.0f - s))));
           uov.e[j] = Elem<T>::from_f32(d * (gf * s));
         }
-        if (dg != nullptr) store16<NT>(dg + i * V, gov.raw);
-        if (du != nullptr) store16<NT>(du + i * V, uov.raw);
+        if constexpr (WT) {
+          const int off = static_cast<int>(i * 16);
+          if (dg != nullptr) __builtin_amdgcn_raw_buffer_store_b128(gov.raw, gbuf, off, 0, kWriteThrough);
+          if (du != nullptr) __builtin_amdgcn_raw_buffer_store_b128(uov.raw, ubuf, off, 0, kWriteThrough);
+        } else {
+          if (dg != nullptr) store16<NT>(dg + i * V, gov.raw);
+          if (du != nullptr) store16<NT>(du + i * V, uov.raw);
+        }
       }
     }
   }
@@ -135,6 +146,10 @@ __global__ __launch_bounds__(256) void swiglu_bwd_elem_kernel(const T* __restric
 // flight and runs 2 workgroups per CU: [16384, 14336] bf16 366-367 us, against 383 us with
 // four vectors at full occupancy and 395-399 us with two at full occupancy.  The forward
 // is fastest with four vectors and no limit (212-216 us at every limit tried).
+// Store policy of the streaming launches (one process, alternated): the backward's two
+// gradients written through L2 (nontemporal, device scope) 361.0 us against 366.3 with
+// nontemporal global stores (364.9 device scope alone, 368.2 nontemporal buffer stores,
+// 366.0 at system scope); the forward's one output 221.3 against 219.0, so it keeps them.
 constexpr int kFwdUnroll = 4;
 constexpr int kBwdUnroll = 2;
 // Streams above this many bytes bypass cache retention (nontemporal).
@@ -209,12 +224,15 @@ void launch_bwd(const void* dy, const void* g, const void* u, void* dg, void* du
   if (nvec > 0) {
     const bool nt = n * static_cast<int64_t>(sizeof(T)) > kNontemporalBytes;
     const unsigned grid = grid_for(nvec, 256 * kBwdUnroll);
-    if (nt) {
-      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, true>, bwd_occupancy(), grid, st, dyp, gp, up,
-                     dgp, dup, nvec);
+    if (nt && nvec <= 0x7fffffff / 16) {
+      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, true, true>, bwd_occupancy(), grid, st, dyp,
+                     gp, up, dgp, dup, nvec);
+    } else if (nt) {
+      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, true, false>, bwd_occupancy(), grid, st, dyp,
+                     gp, up, dgp, dup, nvec);
     } else {
-      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, false>, bwd_occupancy(), grid, st, dyp, gp,
-                     up, dgp, dup, nvec);
+      launch_limited(swiglu_bwd_kernel<T, kBwdUnroll, false, false>, bwd_occupancy(), grid, st,
+                     dyp, gp, up, dgp, dup, nvec);
     }
   }
   const int64_t start = nvec * V;
