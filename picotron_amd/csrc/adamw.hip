@@ -140,6 +140,15 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
   const bool vec_ok = ((r.p | r.g | r.m | r.v) & 15) == 0;
 
   if (vec_ok && end - start == kBlockElems) {
+    // The block's chunk of each stream through a buffer resource, so that the stores can
+    // be written through L2 (nontemporal, device scope): 1.2e9 parameters, one process,
+    // alternated: 5282 against 5290 us per step (one tensor) and 5298 against 5329 (100
+    // tensors) with nontemporal global stores.
+    constexpr int kChunkBytes = static_cast<int>(kBlockElems * 4);
+    const auto pb = uniform_buffer(reinterpret_cast<const void*>(r.p + start * 4), kChunkBytes);
+    const auto mb = uniform_buffer(reinterpret_cast<const void*>(r.m + start * 4), kChunkBytes);
+    const auto vb = uniform_buffer(reinterpret_cast<const void*>(r.v + start * 4), kChunkBytes);
+    const auto gb = uniform_buffer(reinterpret_cast<const void*>(r.g + start * 4), kChunkBytes);
     f32x4 pv[kUnroll], gv[kUnroll], mv[kUnroll], vv[kUnroll];
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
@@ -151,7 +160,6 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
     }
 #pragma unroll
     for (int k = 0; k < kUnroll; ++k) {
-      const int64_t i = start + (static_cast<int64_t>(k) * kThreads + threadIdx.x) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float pp = pv[k][j], mm = mv[k][j], v2 = vv[k][j];
@@ -161,10 +169,12 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restri
         mv[k][j] = mm;
         vv[k][j] = v2;
       }
-      __builtin_nontemporal_store(pv[k], reinterpret_cast<gptr<f32x4>>(P + i));
-      __builtin_nontemporal_store(mv[k], reinterpret_cast<gptr<f32x4>>(M + i));
-      __builtin_nontemporal_store(vv[k], reinterpret_cast<gptr<f32x4>>(Vv + i));
-      if (SCALED && write_grad) __builtin_nontemporal_store(gv[k], reinterpret_cast<gptr<f32x4>>(G + i));
+      const int off = (k * kThreads + static_cast<int>(threadIdx.x)) * 16;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, pv[k]), pb, off, 0, kWriteThrough);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, mv[k]), mb, off, 0, kWriteThrough);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, vv[k]), vb, off, 0, kWriteThrough);
+      if (SCALED && write_grad)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, gv[k]), gb, off, 0, kWriteThrough);
     }
   } else {
     for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
