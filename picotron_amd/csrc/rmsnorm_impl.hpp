@@ -37,8 +37,6 @@ constexpr int kFwdWaves = 4;
 // Cache policy of the row loads (x, dy): nontemporal, the measured optimum on MI355X for data
 // read once per kernel.  The row stores: RowStore.
 constexpr bool kLoadNT = true;
-// Rows the backward keeps in flight ahead of the one it is reducing (0, 1 or 2).
-constexpr int kBwdPrefetch = 1;
 
 // ------------------------------------------------------------------ device helpers
 
@@ -430,7 +428,7 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_finish_kernel(const float* __r
 // same lane).
 
 template <typename T, typename WT, int VPL, int WPR, int WAVES, bool ALIGNED, bool LOAD_NT,
-          bool ADD, int PREFETCH = kBwdPrefetch>
+          bool ADD>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     const T* __restrict__ dy, int64_t dys, const T* __restrict__ x, int64_t xs,
     const void* __restrict__ w, int wdt, const float* __restrict__ rstd, T* dx,
@@ -518,63 +516,30 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_bwd_kernel(
     }
   };
 
+  // The next row is double-buffered in registers.  The loop body issues its two prefetches
+  // unconditionally (both rows are within the block's iterations), so the wait for the row
+  // being reduced counts only that row's loads: a prefetch under a branch would make the
+  // compiler wait for everything at the join.  The last one or two rows are peeled.
   int64_t ra = static_cast<int64_t>(blockIdx.x) * RPB + slot;
-  if constexpr (PREFETCH == 2) {
-    // Two rows in flight ahead of the one being reduced.  Consecutive reductions alternate
-    // the two LDS scratch buffers of row_sum.
-    Buf a, b, c;
-    load(a, ra);
-    if (1 < iters) load(b, ra + group_stride);
-    int rb = 0;
-    for (int it = 0; it < iters; it += 3) {
-      const int64_t r1n = ra + group_stride, r2n = ra + 2 * group_stride;
-      if (it + 2 < iters) load(c, r2n);
-      process(a, ra, rb);
-      rb ^= 1;
-      if (it + 3 < iters) load(a, ra + 3 * group_stride);
-      if (it + 1 < iters) {
-        process(b, r1n, rb);
-        rb ^= 1;
-      }
-      if (it + 4 < iters) load(b, ra + 4 * group_stride);
-      if (it + 2 < iters) {
-        process(c, r2n, rb);
-        rb ^= 1;
-      }
-      ra += 3 * group_stride;
-    }
-  } else if constexpr (PREFETCH == 1) {
-    // The loop body issues its two prefetches unconditionally (both rows are within the
-    // block's iterations), so the wait for the row being reduced counts only that row's
-    // loads: a prefetch under a branch would make the compiler wait for everything at the
-    // join.  The last one or two rows are peeled.
-    Buf a, b;
-    load(a, ra);
-    int it = 0;
-    for (; it + 2 < iters; it += 2) {
-      const int64_t rb = ra + group_stride;
-      load(b, rb);
-      process(a, ra, 0);
-      const int64_t rc = rb + group_stride;
-      load(a, rc);
-      process(b, rb, 1);
-      ra = rc;
-    }
-    if (it + 1 < iters) {
-      const int64_t rb = ra + group_stride;
-      load(b, rb);
-      process(a, ra, 0);
-      process(b, rb, 1);
-    } else {
-      process(a, ra, 0);
-    }
+  Buf a, b;
+  load(a, ra);
+  int it = 0;
+  for (; it + 2 < iters; it += 2) {
+    const int64_t rb = ra + group_stride;
+    load(b, rb);
+    process(a, ra, 0);
+    const int64_t rc = rb + group_stride;
+    load(a, rc);
+    process(b, rb, 1);
+    ra = rc;
+  }
+  if (it + 1 < iters) {
+    const int64_t rb = ra + group_stride;
+    load(b, rb);
+    process(a, ra, 0);
+    process(b, rb, 1);
   } else {
-    for (int it = 0; it < iters; ++it) {
-      Buf a;
-      load(a, ra);
-      process(a, ra, it & 1);
-      ra += group_stride;
-    }
+    process(a, ra, 0);
   }
   if (!want_dw) return;
 
