@@ -60,6 +60,38 @@ def test_swiglu_past_2_31_elements(gpu, extra):
         torch.testing.assert_close(du[w].double(), eu, **BF16)
 
 
+# The write-through stores address a whole output through one buffer resource with 31-bit
+# byte offsets; outputs up to 2^31 - 1 bytes take them, larger ones the nontemporal global
+# stores.  These cases sit at that limit on both sides.
+_WT_VECS = 0x7FFFFFFF // 16  # 16-byte vectors of the largest write-through SwiGLU output
+
+
+@pytest.mark.parametrize("n", [_WT_VECS * 8, _WT_VECS * 8 + 3, (_WT_VECS + 1) * 8])
+def test_swiglu_backward_at_the_write_through_limit(gpu, n):
+    g = _randn(n, torch.bfloat16, gpu, 21)
+    u = _randn(n, torch.bfloat16, gpu, 22)
+    dy = _randn(n, torch.bfloat16, gpu, 23)
+    dg, du = ops.swiglu_bwd(dy, g, u)
+    torch.cuda.synchronize()
+    for w in (slice(0, 1 << 20), slice(n // 2, n // 2 + (1 << 20)), slice(n - (1 << 20), n)):
+        eg, eu = o_swiglu.backward(dy[w], g[w], u[w])
+        torch.testing.assert_close(dg[w].double(), eg, **BF16)
+        torch.testing.assert_close(du[w].double(), eu, **BF16)
+
+
+@pytest.mark.parametrize("s", [4095, 4097])  # output 2^31 - 2^19 bytes / over 2^31 bytes
+def test_rope_at_the_write_through_limit(gpu, s):
+    b, h, d = 64, 32, 128
+    cos, sin = o_rope.tables(s, d, 500_000.0, device=gpu)
+    x = _randn((b, s, h, d), torch.bfloat16, gpu, 24).transpose(1, 2)  # (B,H,S,D) of (B,S,H,D)
+    for layout in ("interleaved", "rotate_half"):
+        y, _ = ops.rope(x, cos, sin, layout=layout)
+        torch.cuda.synchronize()
+        for bi in (0, b - 1):
+            torch.testing.assert_close(y[bi].double(), o_rope.rotate(x[bi], cos, sin, layout), **BF16)
+        del y
+
+
 def test_rmsnorm_past_2_31_elements(gpu):
     cols = 4096
     rows = TWO31 // cols + 13  # the last 13 rows start past element 2^31
