@@ -1976,6 +1976,10 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if "PICOTRON_HIP_LIB" not in os.environ:
+        from picotron_amd.build import ensure_built
+
+        ensure_built()  # only when the in-tree library is missing
     _lib.lib()
     if not ops.device_supported(0):
         print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)

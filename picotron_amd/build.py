@@ -95,6 +95,15 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+def ensure_built() -> Path:
+    """The in-tree library, built first when it is not there.  An existing library is used
+    as it is: after changing a source, call :func:`build`."""
+
+    if not LIB_PATH.exists():
+        build()
+    return LIB_PATH
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("-j", "--jobs", type=int, default=None)

@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
@@ -10,6 +11,16 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT))
 GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def pytest_sessionstart(session: pytest.Session) -> None:
+    """Build the in-tree library once if it is missing (a fresh checkout); an existing one,
+    or one named by PICOTRON_HIP_LIB, is used as it is."""
+
+    if "PICOTRON_HIP_LIB" not in os.environ:
+        from picotron_amd.build import ensure_built
+
+        ensure_built()
 
 
 def pytest_configure(config: pytest.Config) -> None:
