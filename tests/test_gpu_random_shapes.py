@@ -163,7 +163,7 @@ def test_cross_entropy_train_loop_view_random(gpu, case):
         # the backward writes the fp16 gradient at a GradScaler-sized scale (as in _check)
         scale = t_ce._fp16_scale_for(n_valid)
         ops.cross_entropy_scale_grad(bview, targets, torch.full((), scale, device=gpu), workspace=ws)
-        t_ce._fp16_grad_close(bview, ref_grad, scale)
+        t_ce._fp16_grad_close(bview, ref_grad, scale, n_valid)
     else:
         t_ce._grad_close(bview, ref_grad, n_valid, dtype)
     assert torch.equal(buf[:, -1, :], base[:, -1, :])
@@ -196,7 +196,7 @@ def test_shifted_cross_entropy_random(gpu, case):
         scale = t_ce._fp16_scale_for(n_valid)
         ops.cross_entropy_shifted_scale_grad(buf, ids, torch.full((), scale, device=gpu), workspace=ws,
                                              logits=logits if out_of_place else None)
-        t_ce._fp16_grad_close(buf, ref_grad, scale)
+        t_ce._fp16_grad_close(buf, ref_grad, scale, n_valid)
     else:
         t_ce._grad_close(buf, ref_grad, n_valid, dtype)
     assert torch.equal(logits, before)
@@ -214,6 +214,7 @@ def test_adamw_random_parameter_lists(gpu, case):
     seed = 7000 + 1000 * case
     fused = [torch.nn.Parameter(randn((n,), torch.float32, gpu, seed + i, 0.02)) for i, n in enumerate(sizes)]
     ref = [torch.nn.Parameter(p.detach().clone()) for p in fused]
+    initial = [float(p.detach().abs().max()) for p in fused]
     opt_f = torch.optim.AdamW(fused, **hp)
     opt_r = torch.optim.AdamW(ref, foreach=False, **hp)
     for step in range(2):
@@ -226,7 +227,12 @@ def test_adamw_random_parameter_lists(gpu, case):
         else:
             triton_adamw_step(opt_f)
         opt_r.step()
-    for a, r in zip(fused, ref):
-        close_fp32(a.detach(), r.detach())
-        close_fp32(opt_f.state[a]["exp_avg"], opt_r.state[r]["exp_avg"])
+    # A parameter is its initial value minus two updates of about lr each, and exp_avg a sum
+    # of (1 - beta1) * g terms (g ~ 1e-3): either can nearly cancel in a small tensor, so their
+    # absolute floor scales with those summands (the clip coefficient, from a differently
+    # ordered fp32 norm, moves every update in its last bits).  exp_avg_sq sums squares.
+    for a, r, p0 in zip(fused, ref, initial):
+        close_fp32(a.detach(), r.detach(), scale=max(p0, 2 * hp["lr"], float(r.detach().abs().max())))
+        m = opt_r.state[r]["exp_avg"]
+        close_fp32(opt_f.state[a]["exp_avg"], m, scale=max(1e-4, float(m.abs().max())))
         close_fp32(opt_f.state[a]["exp_avg_sq"], opt_r.state[r]["exp_avg_sq"])
