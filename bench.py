@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|ce_train_fp16|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|ce_train_fp16|ce_demo_fp16|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
 
 Default workload (the headline metric, "RMSNorm/SwiGLU fwd+bwd"): ``--layers`` decoder layers
 (default 4), each with its own activations: the RMSNorm forward of a bf16 [16384 tokens
@@ -513,11 +513,13 @@ class HeadlineWorkload(Workload):
         # before the other configurations, whose CPU baselines leave the host cores busy
         # for a while, which slows the host-bound eager steps; a failure here (it runs torch's
         # own kernels and graph capture too) is reported in the line rather than ending it
-        try:
-            quickstart = _quickstart_line(steps=200)
-        except Exception as error:  # noqa: BLE001
-            quickstart = {"error": f"{type(error).__name__}: {error}"}
-        return {"ops": ops_out, "other_configs": _other_configs(steps), "quickstart_step": quickstart}
+        steps_out = {}
+        for key, describe, count in (("quickstart_step", _quickstart_line, 200), ("demo_step", _demo_line, 50)):
+            try:
+                steps_out[key] = describe(steps=count)
+            except Exception as error:  # noqa: BLE001
+                steps_out[key] = {"error": f"{type(error).__name__}: {error}"}
+        return {"ops": ops_out, "other_configs": _other_configs(steps), **steps_out}
 
     def cpu_baseline(self) -> dict:
         rms, swiglu = self.rms.cpu_baseline(), self.swiglu.cpu_baseline()
@@ -552,7 +554,7 @@ def _host_time(step, steps: int, warmup: int = 2) -> float:
 # Whether the secondary lines get their CPU baseline (off with --no-cpu-baseline).
 _WITH_CPU_BASELINE = True
 
-OTHER_CONFIGS = ("rope", "ce", "ce_ref_call", "adamw", "adamw_list", "rmsnorm_fp32")
+OTHER_CONFIGS = ("rope", "ce", "ce_ref_call", "ce_demo_fp16", "adamw", "adamw_list", "rmsnorm_fp32")
 
 
 def _other_configs(steps: int) -> dict:
@@ -560,8 +562,8 @@ def _other_configs(steps: int) -> dict:
     HIP events per dominant launch, HBM traffic from its committed counter summary, CPU
     baseline on a bounded sample) and freed: RoPE (q [8,2048,32,128] + k [8,2048,8,128],
     rotate-half, 4 layers), the fused cross-entropy ([8192, 128256] bf16, in place), the
-    reference's unchanged train-loop call ([4, 2049, 128256] bf16, out of place), the fused
-    AdamW step (1.2e9 fp32 parameters, as one tensor and as 100) and RMSNorm in fp32, the
+    reference's unchanged train-loop call ([4, 2049, 128256] bf16, out of place), the same call
+    on the notebook demo's fp16 logits ([32, 256, 50257], loss x 65536), the fused AdamW step (1.2e9 fp32 parameters, as one tensor and as 100) and RMSNorm in fp32, the
     norms' training dtype ([16384, 4096], 4 layers)."""
 
     out = {}
@@ -934,6 +936,68 @@ class CrossEntropyTrainFp16Workload(CrossEntropyTrainWorkload):
                    f"the fp32 upcast of the sliced view (the reference fallback under fp16 autocast), median "
                    f"of {calls} calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
             seconds_per_call=sec, tokens_per_s=self.b * (s - 1) / sec,
+        )
+
+
+class CrossEntropyDemoFp16Workload(CrossEntropyTrainFp16Workload):
+    """The notebook demo's loss (examples/kaggle_demo_pretrain_sft_dpo.ipynb, cell 4: GPT-2's
+    50257-token vocabulary, micro-batch 32 x sequence 256, fp16 with the train loop's
+    GradScaler) through the reference's call site (train_loop.py:95-97,141-144):
+    ``CrossEntropyWithFallback(use_triton=True)`` on ``logits[:, :-1, :].transpose(1, 2)``
+    against ``input_ids[:, 1:]``, the loss scaled by 65536 before its backward.  A row of 50257
+    fp16 logits is 100514 bytes, so rows start on no common 16-byte or 128-byte boundary: the
+    kernels split each row at its first 128-byte line."""
+
+    name = "ce_demo_fp16"
+    metric = ("Next-token cross-entropy fwd + autograd bwd through the reference's call site (fp16, loss "
+              "scale 65536) HBM GB/s & % of peak, logits [32, 256, 50257]")
+    b, s, vocab = 32, 256, 50257
+
+    def __init__(self, layers: int) -> None:
+        from picotron_amd.nn.triton_kernels import CrossEntropyWithFallback
+
+        super().__init__(layers)
+        b, s, v = self.b, self.s, self.vocab
+        self.loss_function = CrossEntropyWithFallback(use_triton=True)
+        g = torch.Generator(device="cuda").manual_seed(112)
+        self.ids = torch.randint(0, v, (b, s), generator=g, device="cuda")  # pretraining: every target kept
+        # forward: the b * (s - 1) rows read; backward: read again, the gradient of all b * s
+        # rows written (the last position's rows as zeros)
+        self.bytes_per_step = (2 * b * (s - 1) + b * s) * v * 2 + 16 * b * s
+        self.tokens_per_step = b * (s - 1)
+        self.dominant = ("cross-entropy of the reference's call, fp16: ce_prepare_kernel + ce_lse_kernel + "
+                         "ce_finish_kernel, then ce_scale_kernel writing the scaled gradient to a new buffer")
+        self.dominant_bytes = self.bytes_per_step
+        self.description = (
+            f"the reference's train-loop call on fp16 model logits [{b}, {s}, {v}] ~N(0,2^2): "
+            f"CrossEntropyWithFallback(use_triton=True)(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:]), "
+            f"loss x 65536 (a GradScaler's scale) before torch.autograd.grad to the logits' leaf; the logits are "
+            f"left untouched and the gradient goes to a new buffer"
+        )
+
+    def _step(self, shifted: bool):
+        logits = self.leaf.view(self.b, self.s, self.vocab)
+        loss = self.loss_function(logits[:, :-1, :].transpose(1, 2), self.ids[:, 1:])
+        (grad,) = torch.autograd.grad(loss * self.loss_scale, self.leaf)
+        return grad
+
+    def cpu_baseline(self) -> dict:
+        from oracle import cross_entropy as o_ce
+
+        cores, _, _ = _cpu_info()
+        torch.set_num_threads(cores)
+        nb = 4
+        logits = self.leaf.detach()[:nb].cpu()
+        ids = self.ids[:nb].cpu()
+        sec, calls = _time_cpu(lambda: o_ce.fallback_forward_backward(
+            logits[:, :-1, :].transpose(1, 2), ids[:, 1:]))
+        return dict(
+            value=((2 * nb * (self.s - 1) + nb * self.s) * self.vocab * 2 + 16 * nb * self.s) / sec / 1e9,
+            unit="GB/s", cores=cores, kind="port",
+            sample=f"first {nb} of the {self.b} sequences, fp16 logits: F.cross_entropy fwd + autograd bwd on "
+                   f"the fp32 upcast of the sliced view (the reference fallback under fp16 autocast), median "
+                   f"of {calls} calls (~{CPU_TARGET_S:.0f} s) after 1 warm-up",
+            seconds_per_call=sec, tokens_per_s=nb * (self.s - 1) / sec,
         )
 
 
@@ -1570,46 +1634,71 @@ class CopyWorkload(Workload):
         return None
 
 
-# ------------------------------------------------------------------ quickstart training step
+# ------------------------------------------------------------------ whole training steps
 
 # The reference's quickstart model and batch (src/picotron/config/picotron_decoder.yaml:7-10,
 # 16-19): vocabulary 64, hidden 32, intermediate 64, 2 layers, 4 heads, sequence 16, micro-batch 2,
 # learning rate 1e-3; AdamW betas (0.9, 0.999), eps 1e-8, weight decay 0 and no clipping are the
-# config defaults (src/picotron/config/config.py:360-366,384-385).
-QUICKSTART = dict(vocab=64, hidden=32, intermediate=64, layers=2, heads=4, seq=16, batch=2, lr=1e-3)
+# config defaults (src/picotron/config/config.py:360-366,384-385); bf16 autocast is what
+# `dtype: auto` resolves to on a bf16 GPU (train_loop.py:57,274-282).
+QUICKSTART = dict(vocab=64, hidden=32, intermediate=64, layers=2, heads=4, kv_heads=4, seq=16, batch=2,
+                  lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0, clip=None, dtype="bf16",
+                  theta=10_000.0, window=None, nope=(), tied=False)
+# The notebook's pretraining run (examples/kaggle_demo_pretrain_sft_dpo.ipynb, cell 4): vocabulary
+# 50257, hidden 20, intermediate 80, 8 layers, 2 heads over 1 key/value head, RoPE theta 1e6 except
+# on layer 3, a 128-token sliding window, tied embeddings, sequence 256 x micro-batch 32, fp16
+# with the train loop's GradScaler (train_loop.py:155-160), AdamW lr 3e-4, betas (0.9, 0.95),
+# weight decay 0.1, gradients clipped to 1.0.
+DEMO_1M = dict(vocab=50257, hidden=20, intermediate=80, layers=8, heads=2, kv_heads=1, seq=256, batch=32,
+               lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, clip=1.0, dtype="fp16",
+               theta=1e6, window=128, nope=(3,), tied=True)
 QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused",
                        "graph_fused_residual")
+# fp16 with a GradScaler reads the overflow flag on the host every step: eager only
+DEMO_VARIANTS = ("eager_reference", "eager_fused_modules", "eager_fused")
+STEP_VARIANTS = ("eager_reference", "eager_fused_modules", "eager_fused", "graph_reference", "graph_fused",
+                 "graph_fused_residual")
 
 
-class _QuickstartBlock(torch.nn.Module):
+class _StepBlock(torch.nn.Module):
     """The reference's decoder block (src/picotron/models/picotron_decoder.py:70-130): attention
     norm, causal self-attention (src/picotron/nn/attention.py: bias-free q/k/v/o projections,
-    heads split to (B, H, S, D), RoPE on q and k, SDPA under a boolean causal mask), residual add,
-    MLP norm, SwiGLU MLP, residual add.  The attention product runs in fp32 in every variant
-    (plain PyTorch, identical between them)."""
+    heads split to (B, H, S, D), RoPE on q and k unless the layer has none, key/value heads
+    repeated for grouped-query attention, SDPA under a boolean causal or sliding-window mask),
+    residual add, MLP norm, SwiGLU MLP, residual add.  The attention product runs in fp32 in
+    every variant (plain PyTorch, identical between them)."""
 
-    def __init__(self, fused: bool) -> None:
+    def __init__(self, cfg: dict, fused: bool, use_rope: bool) -> None:
         from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU
 
         super().__init__()
-        h, heads = QUICKSTART["hidden"], QUICKSTART["heads"]
-        self.heads, self.head_dim = heads, h // heads
+        h, heads, kv = cfg["hidden"], cfg["heads"], cfg["kv_heads"]
+        self.heads, self.kv_heads, self.head_dim, self.window = heads, kv, h // heads, cfg["window"]
         self.attention_norm = RMSNorm(h, use_triton_rmsnorm=fused)
         self.query_projection = torch.nn.Linear(h, h, bias=False)
-        self.key_projection = torch.nn.Linear(h, h, bias=False)
-        self.value_projection = torch.nn.Linear(h, h, bias=False)
+        self.key_projection = torch.nn.Linear(h, kv * self.head_dim, bias=False)
+        self.value_projection = torch.nn.Linear(h, kv * self.head_dim, bias=False)
         self.output_projection = torch.nn.Linear(h, h, bias=False)
-        self.rotary_embedding = RotaryEmbedding(self.head_dim, 10_000.0, use_triton_rope=fused)
+        self.rotary_embedding = (RotaryEmbedding(self.head_dim, cfg["theta"], use_triton_rope=fused)
+                                 if use_rope else None)
         self.mlp_norm = RMSNorm(h, use_triton_rmsnorm=fused)
-        self.mlp = SwiGLU(h, QUICKSTART["intermediate"], use_triton_swiglu=fused)
+        self.mlp = SwiGLU(h, cfg["intermediate"], use_triton_swiglu=fused)
 
     def _attention(self, x: torch.Tensor) -> torch.Tensor:
         b, s, h = x.shape
-        split = lambda t: t.view(b, s, self.heads, self.head_dim).transpose(1, 2)  # noqa: E731
-        q, k = self.rotary_embedding(split(self.query_projection(x)), split(self.key_projection(x)))
-        v = split(self.value_projection(x))
+        split = lambda t, n: t.view(b, s, n, self.head_dim).transpose(1, 2)  # noqa: E731
+        q = split(self.query_projection(x), self.heads)
+        k = split(self.key_projection(x), self.kv_heads)
+        v = split(self.value_projection(x), self.kv_heads)
+        if self.rotary_embedding is not None:
+            q, k = self.rotary_embedding(q, k)
+        if self.kv_heads != self.heads:
+            k = k.repeat_interleave(self.heads // self.kv_heads, dim=1)
+            v = v.repeat_interleave(self.heads // self.kv_heads, dim=1)
         positions = torch.arange(s, device=x.device)
         mask = positions.unsqueeze(0) <= positions.unsqueeze(1)
+        if self.window is not None:
+            mask &= positions.unsqueeze(0) >= positions.unsqueeze(1) - self.window + 1
         out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask,
                                              scale=self.head_dim ** -0.5)
         return self.output_projection(out.to(q.dtype).transpose(1, 2).reshape(b, s, h))
@@ -1629,21 +1718,28 @@ class _QuickstartBlock(torch.nn.Module):
         return next_norm.add_and_norm(self.mlp(normed).to(hidden.dtype), hidden)
 
 
-class _QuickstartDecoder(torch.nn.Module):
+class _StepDecoder(torch.nn.Module):
     """The reference's decoder (src/picotron/models/picotron_decoder.py:133-220) with RoPE
-    positions and an untied output projection, built from this package's modules; ``fused``
-    sets every module's kernel flag, as ``model.triton_kernels`` does."""
+    positions, built from this package's modules; ``fused`` sets every module's kernel flag, as
+    ``model.triton_kernels`` does.  A tied output projection uses the token embeddings' weight
+    (`TiedOutputProjection`, picotron_decoder.py:49-67)."""
 
-    def __init__(self, fused: bool, residual: bool = False) -> None:
+    def __init__(self, cfg: dict, fused: bool, residual: bool = False) -> None:
         from picotron_amd.nn import RMSNorm
 
         super().__init__()
         self.residual = residual
-        v, h = QUICKSTART["vocab"], QUICKSTART["hidden"]
+        v, h = cfg["vocab"], cfg["hidden"]
         self.token_embeddings = torch.nn.Embedding(v, h)
-        self.layers = torch.nn.ModuleList(_QuickstartBlock(fused) for _ in range(QUICKSTART["layers"]))
+        self.layers = torch.nn.ModuleList(_StepBlock(cfg, fused, i not in cfg["nope"])
+                                          for i in range(cfg["layers"]))
         self.final_norm = RMSNorm(h, use_triton_rmsnorm=fused)
-        self.output_projection = torch.nn.Linear(h, v, bias=False)
+        self.output_projection = None if cfg["tied"] else torch.nn.Linear(h, v, bias=False)
+
+    def _project(self, hidden: torch.Tensor) -> torch.Tensor:
+        if self.output_projection is None:
+            return F.linear(hidden, self.token_embeddings.weight)
+        return self.output_projection(hidden)
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         hidden = self.token_embeddings(input_ids)
@@ -1652,52 +1748,77 @@ class _QuickstartDecoder(torch.nn.Module):
             norms = [layer.attention_norm for layer in self.layers[1:]] + [self.final_norm]
             for layer, next_norm in zip(self.layers, norms):
                 hidden, normed = layer.forward_residual(hidden, normed, next_norm)
-            return self.output_projection(normed)
+            return self._project(normed)
         for layer in self.layers:
             hidden = layer(hidden)
-        return self.output_projection(self.final_norm(hidden))
+        return self._project(self.final_norm(hidden))
 
 
-class QuickstartTrainer:
-    """One training step of the quickstart model as the train loop runs it
-    (src/picotron/training/train_loop.py:134-168, the plain AdamW branch): zero_grad, forward and
-    the next-token loss on the (B, V, S-1) logits view under bf16 autocast (what ``dtype: auto``
-    resolves to on a bf16 GPU, train_loop.py:57,274-282), backward, optimizer step.
+class StepTrainer:
+    """One training step of a decoder config as the train loop runs it
+    (src/picotron/training/train_loop.py:134-168): zero_grad, forward and the next-token loss on
+    the (B, V, S-1) logits view under autocast, backward, then the update: the plain branch
+    (clip if configured, optimizer step; :165-168) or, for fp16, the GradScaler branch (scale,
+    backward, unscale_, clip, step, update; :155-160).
 
     ``variant``: ``eager_reference`` runs the modules with their kernel flags off, torch's loss
-    and torch's AdamW step (the reference's fallbacks); ``eager_fused`` the same model with every
-    flag on, ``CrossEntropyWithFallback(use_triton=True)`` and ``AdamWStepWithFallback``;
-    the ``graph_*`` variants capture that whole step in one HIP graph (capturable AdamW,
-    gradients zeroed in place so that their addresses stay fixed) and replay it.
-    ``graph_fused_residual`` also fuses each residual add into the norm after it
-    (``RMSNorm.add_and_norm``), a change to the model's code rather than a flag.  ``capturable``
-    overrides the optimizer's flag (by default set for the graph variants only)."""
+    and torch's update (the reference's fallbacks); ``eager_fused_modules`` turns on the module
+    flags only (RMSNorm, SwiGLU and RoPE); ``eager_fused`` every flag, with
+    ``CrossEntropyWithFallback(use_triton=True)`` and the fused update of
+    ``AdamWStepWithFallback`` (``step(optimizer, max_grad_norm=)`` or ``step_with_grad_scaler``);
+    the ``graph_*`` variants (bf16 configs) capture the whole step in one HIP graph
+    (capturable AdamW, gradients zeroed in place so that their addresses stay fixed) and
+    replay it; ``graph_fused_residual`` also fuses each residual add into the norm after it
+    (``RMSNorm.add_and_norm``), a change to the model's code rather than a flag.
+    ``capturable`` overrides the optimizer's flag (by default set for the graph variants)."""
 
-    def __init__(self, variant: str, seed: int = 1337, capturable: bool | None = None) -> None:
+    def __init__(self, cfg: dict, variant: str, seed: int = 1337, capturable: bool | None = None) -> None:
         from picotron_amd.nn.triton_kernels import AdamWStepWithFallback, CrossEntropyWithFallback
 
-        if variant not in QUICKSTART_VARIANTS:
+        if variant not in STEP_VARIANTS:
             raise ValueError(f"unknown variant {variant}")
-        self.variant = variant
-        fused = "fused" in variant
+        self.cfg, self.variant = cfg, variant
         self.graphed = variant.startswith("graph")
+        if self.graphed and cfg["dtype"] == "fp16":
+            raise ValueError("the GradScaler step reads its overflow flag on the host: not capturable")
+        fused_modules = "fused" in variant
+        self.fused_update = fused_modules and not variant.endswith("modules")
+        self.autocast = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float16
         torch.manual_seed(seed)
-        self.model = _QuickstartDecoder(fused, residual=variant.endswith("residual")).cuda()
-        self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=QUICKSTART["lr"], betas=(0.9, 0.999),
-                                           eps=1e-8, weight_decay=0.0,
+        self.model = _StepDecoder(cfg, fused_modules, residual=variant.endswith("residual")).cuda()
+        self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=cfg["lr"], betas=cfg["betas"],
+                                           eps=1e-8, weight_decay=cfg["weight_decay"],
                                            capturable=self.graphed if capturable is None else capturable)
-        self.loss_function = CrossEntropyWithFallback(use_triton=fused)
-        self.optimizer_step = AdamWStepWithFallback(use_triton=fused)
+        self.scaler = torch.amp.GradScaler("cuda") if cfg["dtype"] == "fp16" else None
+        self.loss_function = CrossEntropyWithFallback(use_triton=self.fused_update)
+        self.optimizer_step = AdamWStepWithFallback(use_triton=self.fused_update)
         self.graph = None
         self.static_ids = None
 
     def _step(self, input_ids: torch.Tensor) -> torch.Tensor:
+        clip = self.cfg["clip"]
         self.optimizer.zero_grad(set_to_none=not self.graphed)
-        with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=not self.graphed):
+        with torch.autocast("cuda", dtype=self.autocast, cache_enabled=not self.graphed):
             logits = self.model(input_ids)
             loss = self.loss_function(logits[:, :-1, :].transpose(1, 2), input_ids[:, 1:])
-        loss.backward()
-        self.optimizer_step.step(self.optimizer)
+        if self.scaler is not None:
+            self.scaler.scale(loss).backward()
+            if self.fused_update:
+                self.optimizer_step.step_with_grad_scaler(self.scaler, self.optimizer, clip)
+            else:
+                self.scaler.unscale_(self.optimizer)
+                if clip is not None:
+                    torch.nn.utils.clip_grad_norm_(self.model.parameters(), clip)
+                self.scaler.step(self.optimizer)
+                self.scaler.update()
+        else:
+            loss.backward()
+            if self.fused_update and clip is not None:
+                self.optimizer_step.step(self.optimizer, max_grad_norm=clip)
+            else:
+                if clip is not None:
+                    torch.nn.utils.clip_grad_norm_(self.model.parameters(), clip)
+                self.optimizer_step.step(self.optimizer)
         return loss.detach()
 
     def prepare(self, input_ids: torch.Tensor, warmup: int = 3) -> None:
@@ -1735,32 +1856,58 @@ class QuickstartTrainer:
         return self.static_loss
 
 
+class QuickstartTrainer(StepTrainer):
+    """:class:`StepTrainer` on the quickstart config."""
+
+    def __init__(self, variant: str, seed: int = 1337, capturable: bool | None = None) -> None:
+        super().__init__(QUICKSTART, variant, seed, capturable)
+
+
+def _describe(cfg: dict) -> str:
+    return (f"vocab {cfg['vocab']}, hidden {cfg['hidden']}, intermediate {cfg['intermediate']}, "
+            f"{cfg['layers']} layers, {cfg['heads']} heads / {cfg['kv_heads']} key-value heads, "
+            f"micro-batch {cfg['batch']} x sequence {cfg['seq']}, {cfg['dtype']} autocast"
+            + (", GradScaler" if cfg["dtype"] == "fp16" else "")
+            + (f", clip {cfg['clip']}" if cfg["clip"] is not None else "")
+            + (f", sliding window {cfg['window']}" if cfg["window"] else "")
+            + (", tied embeddings" if cfg["tied"] else ""))
+
+
 def _quickstart_line(steps: int) -> dict:
     """The quickstart step figures with what they describe (a section of the default line)."""
 
-    q = QUICKSTART
     return {
-        "workload": (f"one training step of the quickstart decoder (vocab {q['vocab']}, hidden {q['hidden']}, "
-                     f"intermediate {q['intermediate']}, {q['layers']} layers, {q['heads']} heads), micro-batch "
-                     f"{q['batch']} x sequence {q['seq']}, bf16 autocast: zero_grad, forward, next-token loss on "
-                     f"the (B, V, S-1) view, backward, AdamW step; batches resident on the device"),
+        "workload": ("one training step of the quickstart decoder (" + _describe(QUICKSTART) + "): zero_grad, "
+                     "forward, next-token loss on the (B, V, S-1) view, backward, AdamW step; batches resident "
+                     "on the device"),
         "steps": steps,
-        "variants": quickstart_step_figures(steps),
+        "variants": step_figures(QUICKSTART, steps, QUICKSTART_VARIANTS),
     }
 
 
-def quickstart_step_figures(steps: int = 200, variants=QUICKSTART_VARIANTS) -> dict:
+def _demo_line(steps: int) -> dict:
+    """The notebook demo's step figures with what they describe (a section of the default line)."""
+
+    return {
+        "workload": ("one training step of the notebook's pretraining model (" + _describe(DEMO_1M) + "): "
+                     "zero_grad, forward, next-token loss on the (B, V, S-1) view, scaled backward, unscale + "
+                     "clip + AdamW step + scaler update; batches resident on the device"),
+        "steps": steps,
+        "variants": step_figures(DEMO_1M, steps, DEMO_VARIANTS),
+    }
+
+
+def step_figures(cfg: dict, steps: int, variants) -> dict:
     """Per variant: the host time to issue one step, the wall time per step when steps are
     issued back to back (the slower of host and device sets it), the device time per step
     between HIP events around those steps, and the wall time per step in the train loop's own
     form, which reads the loss back after every step (train_loop.py:169)."""
 
     g = torch.Generator(device="cuda").manual_seed(5)
-    batches = torch.randint(0, QUICKSTART["vocab"], (steps, QUICKSTART["batch"], QUICKSTART["seq"]),
-                            generator=g, device="cuda")
+    batches = torch.randint(0, cfg["vocab"], (steps, cfg["batch"], cfg["seq"]), generator=g, device="cuda")
     out = {}
     for variant in variants:
-        trainer = QuickstartTrainer(variant)
+        trainer = StepTrainer(cfg, variant)
         trainer.prepare(batches[0])
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -1783,6 +1930,7 @@ def quickstart_step_figures(steps: int = 200, variants=QUICKSTART_VARIANTS) -> d
             "train_loop_us_per_step": round(loop / steps * 1e6, 1),
         }
         del trainer
+        torch.cuda.empty_cache()
     return out
 
 
@@ -1797,6 +1945,7 @@ WORKLOADS = {
     "ce_train": CrossEntropyTrainWorkload,
     "ce_ref_call": CrossEntropyReferenceCallWorkload,
     "ce_train_fp16": CrossEntropyTrainFp16Workload,
+    "ce_demo_fp16": CrossEntropyDemoFp16Workload,
     "adamw": AdamWWorkload,
     "adamw_list": AdamWListWorkload,
     "adamw_clip": AdamWClipWorkload,
@@ -1806,7 +1955,7 @@ WORKLOADS = {
     "copy": CopyWorkload,
 }
 
-DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "rmsnorm_fp32": 4, "ce_ref_call": 1, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "ce_train_fp16": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
+DEFAULT_LAYERS = {"headline": 4, "rmsnorm": 4, "rmsnorm_fp32": 4, "ce_ref_call": 1, "residual_rmsnorm": 4, "swiglu": 2, "rope": 4, "ce": 1, "ce_train": 1, "ce_train_fp16": 1, "ce_demo_fp16": 1, "adamw": 1, "adamw_list": 1, "adamw_clip": 1,
                   "zero_step": 1, "fp16_step": 1, "modules": 1, "copy": 4}
 
 
@@ -1920,19 +2069,27 @@ def _cpu_line(wl: Workload) -> dict | None:
     return cpu
 
 
-def _quickstart_main(args) -> int:
-    """The quickstart training step as its own line: value = tokens per second of the
-    graph-captured fused step (or of the one variant asked for), steps issued back to back."""
+def _step_main(args) -> int:
+    """A whole training step as its own line: value = tokens per second of the lead variant
+    (the graph-captured fused step for the quickstart model, the fused eager step for the
+    notebook's fp16 model) or of the one variant asked for, steps issued back to back."""
 
-    variants = QUICKSTART_VARIANTS if args.variant == "all" else (args.variant,)
-    line = _quickstart_line(args.steps) if args.variant == "all" else {
-        "steps": args.steps, "variants": quickstart_step_figures(args.steps, variants)}
+    demo = args.workload == "demo_step"
+    cfg, allowed = (DEMO_1M, DEMO_VARIANTS) if demo else (QUICKSTART, QUICKSTART_VARIANTS)
+    if args.variant != "all" and args.variant not in allowed:
+        print(f"{args.workload}: variant {args.variant} is not one of {', '.join(allowed)}", file=sys.stderr)
+        return 2
+    variants = allowed if args.variant == "all" else (args.variant,)
+    describe = _demo_line if demo else _quickstart_line
+    line = describe(args.steps) if args.variant == "all" else {
+        "steps": args.steps, "variants": step_figures(cfg, args.steps, variants)}
     figs = line["variants"]
-    lead = "graph_fused" if "graph_fused" in figs else variants[0]
+    lead = next((v for v in ("graph_fused", "eager_fused") if v in figs), variants[0])
     us = figs[lead]["wall_us_per_step"]
-    tokens = QUICKSTART["batch"] * QUICKSTART["seq"]
+    tokens = cfg["batch"] * cfg["seq"]
+    name = "notebook demo decoder" if demo else "quickstart decoder"
     result = {
-        "metric": f"quickstart decoder training step ({lead}), tokens/s",
+        "metric": f"{name} training step ({lead}), tokens/s",
         "value": round(tokens / (us * 1e-6), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -1942,10 +2099,10 @@ def _quickstart_main(args) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": cfg["dtype"],
         "data": "synthetic token ids (seeded on device)",
         "config": {"tokens_per_step": tokens, "parallelism": "single GPU", **line},
-        # a few microseconds of work per kernel: launch latency, not HBM, bounds this step
+        # a few microseconds of work per kernel: launch latency, not HBM, bounds these steps
         "roofline": None,
         "cpu_baseline": None,
     }
@@ -1958,9 +2115,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted([*WORKLOADS, "quickstart_step"]), default="headline")
-    parser.add_argument("--variant", choices=("all", *QUICKSTART_VARIANTS), default="all",
-                        help="quickstart_step only: the step variant(s) to time")
+    parser.add_argument("--workload", choices=sorted([*WORKLOADS, "quickstart_step", "demo_step"]),
+                        default="headline")
+    parser.add_argument("--variant", choices=("all", *STEP_VARIANTS), default="all",
+                        help="quickstart_step and demo_step only: the step variant(s) to time")
     parser.add_argument("--layers", type=int, default=None)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra", action="store_true",
@@ -1985,8 +2143,8 @@ def main() -> int:
         print("GPU 0 is not a gfx950 (MI355X) device", file=sys.stderr)
         return 2
 
-    if args.workload == "quickstart_step":
-        return _quickstart_main(args)
+    if args.workload in ("quickstart_step", "demo_step"):
+        return _step_main(args)
     global _WITH_CPU_BASELINE
     _WITH_CPU_BASELINE = not args.no_cpu_baseline
     layers = args.layers or DEFAULT_LAYERS[args.workload]

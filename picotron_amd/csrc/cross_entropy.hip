@@ -266,6 +266,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_buffer(void* base, int byt
 template <typename T>
 constexpr float kExpScale = std::is_same<T, _Float16>::value ? 32768.0f : 1.0f;
 
+// A cache line: the row kernels start their 16-byte vectors on one, so that each wave's
+// 1024-byte access covers 8 whole lines rather than 9 partial ones.
+constexpr int kLineBytes = 128;
+
 // The bit pattern of two / one -inf in the storage type, for masking vectors past the row.
 template <typename T>
 constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000u
@@ -285,11 +289,19 @@ constexpr uint32_t kNegInfWord = std::is_same<T, float>::value      ? 0xff800000
 //      vector store of that address, the target element (softmax_t - 1) / n_valid.
 // Keeping e rounds the softmax twice in 16-bit storage (once as e, once as the gradient),
 // a relative error of at most 2 units of the storage type's last place.
-// The launch picks the smallest VPT of 1, 2, 3, 4, 6, 8, 10, 12, 14, 16 that covers the row;
-// each is at most twice the one before, so the vectors of chunks k < VPT / 2 are always
+// The launch picks the smallest VPT of 1, 2, 3, 4, 6, 7, 8, 10, 12, 14, 16 that covers the
+// row; each is at most twice the one before, so the vectors of chunks k < VPT / 2 are always
 // inside it.
+// Up to 64 VGPRs a CU holds two of these workgroups, one loading while the other reduces or
+// stores: bf16 rows of 32000 and 48000 logits (VPT 4 and 6, 53 and 62 VGPRs) stream at
+// 6.1-6.2 TB/s against 4.8 TB/s for 50256 (VPT 8 online: 77 VGPRs, one workgroup).  VPT 7
+// and 8 therefore take the thread's max over all its vectors first and every exp against
+// that one reference (kMaxFirst: no per-chunk maxima to keep), which brings them under 64.
+template <int VPT>
+constexpr bool kMaxFirst = VPT == 7 || VPT == 8;
+
 template <typename T, int VPT>
-__global__ __launch_bounds__(kThreads) void ce_rows_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMaxFirst<VPT> ? 8 : 1))) void ce_rows_kernel(
     const T* logits, T* grad, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
     int64_t gos, int64_t gis, int vocab, const int64_t* __restrict__ targets, int64_t tos,
     int64_t tis, int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
@@ -344,35 +356,68 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
 
   float m = -INFINITY, s = 0.0f;
-  float mk[VPT];  // running max after chunk k: the reference of the exps kept for chunk k
-#pragma unroll
-  for (int k = 0; k < VPT; ++k) {
+  // the reference of the exps kept for chunk k: the running max after it (online), or the
+  // thread's max over all its chunks (kMaxFirst, one entry)
+  constexpr bool kFirst = kMaxFirst<VPT>;
+  float mk[kFirst ? 1 : VPT];
+  const auto masked = [&](int k) -> Vec16<T> {
     Vec16<T> r = v[k];
     if (k >= VPT / 2 && (tid + k * kThreads) * V >= vocab) {
       const uint32_t ninf = kNegInfWord<T>;
       r.raw = u32x4{ninf, ninf, ninf, ninf};
     }
-    float x[V];
+    return r;
+  };
+  if constexpr (kFirst) {
 #pragma unroll
-    for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
-    float cm = x[0];
+    for (int k = 0; k < VPT; ++k) {
+      const Vec16<T> r = masked(k);
 #pragma unroll
-    for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
-    const float nm = fmaxf(m, cm);
-    const float ref = nm == -INFINITY ? 0.0f : nm;
-    float add = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float e = exp_shifted(x[i], ref);
-      add += e;
-      v[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      for (int i = 0; i < V; ++i) m = fmaxf(m, Elem<T>::to_f32(r.e[i]));
     }
-    // Packed here: left to itself the optimiser would carry the fp32 exps across the
-    // barrier into the gradient branch, twice the registers.
-    asm volatile("" : "+v"(v[k].raw));
-    s = s * exp_shifted(m, ref) + add;
-    m = nm;
-    mk[k] = nm;
+    const float ref = m == -INFINITY ? 0.0f : m;
+    // The exps convert the packed vectors again rather than keep the first pass's fp32
+    // values, which would take VPT * V registers.
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) asm volatile("" : "+v"(v[k].raw));
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const Vec16<T> r = masked(k);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float e = exp_shifted(Elem<T>::to_f32(r.e[i]), ref);
+        s += e;
+        v[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      }
+      asm volatile("" : "+v"(v[k].raw));  // packed here, as below
+    }
+    mk[0] = m;
+  } else {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const Vec16<T> r = masked(k);
+      float x[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
+      float cm = x[0];
+#pragma unroll
+      for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
+      const float nm = fmaxf(m, cm);
+      const float ref = nm == -INFINITY ? 0.0f : nm;
+      float add = 0.0f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float e = exp_shifted(x[i], ref);
+        add += e;
+        v[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      }
+      // Packed here: left to itself the optimiser would carry the fp32 exps across the
+      // barrier into the gradient branch, twice the registers.
+      asm volatile("" : "+v"(v[k].raw));
+      s = s * exp_shifted(m, ref) + add;
+      m = nm;
+      mk[k] = nm;
+    }
   }
   // Max first, then one rescale per partial sum (a max of -inf is shifted by 0, as above).
   const float mw = wave_max(m);
@@ -399,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
     Vec16<T> out;
     // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf (it held only
     // -inf logits, whose exps are 0).
-    const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
+    const float f = exp_shifted(mk[kFirst ? 0 : k], M) * (scale / kExpScale<T>);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(v[k].e[i]) * f);
@@ -424,16 +469,19 @@ __global__ __launch_bounds__(kThreads) void ce_rows_kernel(
   }
 }
 
-// Forward without a gradient write (no gradient, or the fp16 deferred one) over 16-byte
-// aligned rows: a read-only pass, so nothing of the row has to stay in registers and
-// 256-thread workgroups (46-73 VGPRs) share a CU six or more at a time, each streaming its
-// own row; the register-resident kernel, one 1024-thread workgroup per CU, leaves the CU's
-// loads idle while it reduces a row when there is no store phase to overlap.  Per thread,
-// batches of kLseBatch 16-byte nontemporal loads (raw buffer loads: the range check returns
-// zeros past the row, masked to -inf here) feed an online max / sum-exp with one rescale
-// per batch; the wave and block reductions are those of ce_rows_kernel.  Thread 0 reads
-// the target logit at the start (in flight with the row) and writes the row loss and, for a
-// deferred gradient, the row's log-sum-exp.
+// Forward without a gradient write (no gradient, or the fp16 deferred one): a read-only
+// pass, so nothing of the row has to stay in registers and 256-thread workgroups (46-73
+// VGPRs) share a CU six or more at a time, each streaming its own row; the register-resident
+// kernel, one 1024-thread workgroup per CU, leaves the CU's loads idle while it reduces a
+// row when there is no store phase to overlap.  A row is split as in the batched kernel: a
+// head of up to V-1 elements before its first 16-byte boundary and a tail of up to V-1
+// after its last (one element per thread, folded in before the body), and a body of 16-byte
+// vectors (all of an aligned row).  Per thread, batches of kLseBatch 16-byte nontemporal
+// loads of the body (raw buffer loads: the range check returns zeros past the body, masked
+// to -inf here) feed an online max / sum-exp with one rescale per batch; the wave and block
+// reductions are those of ce_rows_kernel.  Thread 0 reads the target logit at the start (in
+// flight with the row) and writes the row loss and, for a deferred gradient, the row's
+// log-sum-exp.
 constexpr int kLseThreads = 256;
 constexpr int kLseWaves = kLseThreads / 64;
 constexpr int kLseBatch = 8;
@@ -464,10 +512,22 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
       xt = Elem<T>::to_f32(p[cur.tgt]);
     }
   }
-  const int row_bytes = vocab * static_cast<int>(sizeof(T));
-  const int nvec = row_bytes / 16;
-  const auto buf = row_buffer(const_cast<T*>(p), row_bytes);
+  // head [0, head): the elements before the row's first 128-byte line, as in the batched
+  // kernel; body [head, head + nvec * V); tail [head + nvec * V, vocab)
+  const int lead = static_cast<int>(((kLineBytes - (reinterpret_cast<uintptr_t>(p) & (kLineBytes - 1))) &
+                                     (kLineBytes - 1)) / sizeof(T));
+  const int head = lead < vocab ? lead : vocab;
+  const int nvec = (vocab - head) / V;
+  const int tail_start = head + nvec * V;
+  const auto buf = row_buffer(const_cast<T*>(p) + head, nvec * 16);
   float m = -INFINITY, s = 0.0f;
+  if (tid < head || tid < vocab - tail_start) {
+    const float a = tid < head ? Elem<T>::to_f32(p[tid]) : -INFINITY;
+    const float b = tid < vocab - tail_start ? Elem<T>::to_f32(p[tail_start + tid]) : -INFINITY;
+    m = fmaxf(a, b);
+    const float ref = m == -INFINITY ? 0.0f : m;
+    s = exp_shifted(a, ref) + exp_shifted(b, ref);
+  }
   for (int base = tid; base < nvec; base += kLseThreads * kLseBatch) {
     Vec16<T> v[kLseBatch];
 #pragma unroll
@@ -515,12 +575,16 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
   }
 }
 
-// Rows that the register-resident kernel does not take -- longer than it holds, or not
-// 16-byte aligned -- with row_bytes + kStreamBatchBytes < 2^31: one 1024-thread workgroup
-// per row in two passes.  A row is split into a head of up to V-1 elements before its first
-// 16-byte boundary (one per thread, from thread 0), a body of 16-byte vectors read in
-// batches of kStreamBatch per thread with raw buffer loads (the hardware range check drops
-// the ragged end), and a tail of up to V-1 elements (one per thread, from the last thread).
+// Rows that the register-resident kernel does not take -- longer than it holds, or, up to
+// 8 vectors per thread, not starting on a 128-byte cache line -- with row_bytes +
+// kStreamBatchBytes < 2^31: one 1024-thread workgroup per row in two passes.  A row is split
+// into a head of the elements before its first 128-byte boundary (at most 127 bytes' worth,
+// one per thread, from thread 0), a body of 16-byte vectors read in batches of kStreamBatch
+// per thread with raw buffer loads (the hardware range check drops the ragged end), and a
+// tail of up to V-1 elements (one per thread, from the last thread).  Starting the body on a
+// line makes each wave's 1024-byte access cover 8 whole lines rather than 9 partial ones: a
+// [8160, V] bf16 forward streams at 5.8-6.0 TB/s for V a multiple of 64 and 4.7-4.9 TB/s for
+// other multiples of 8 when the body starts at the row (50000, 50256, 54000, 57000, 62000).
 //   1. cached loads (the row stays in the Infinity Cache for pass 2) and an online max /
 //      sum per thread, reduced as in ce_rows_kernel (one barrier);
 //   2. the row re-read (nontemporal: last use), exp(x - M) / (S * n_valid) written over it;
@@ -532,8 +596,11 @@ constexpr int kStreamBatchBytes = kStreamBatch * kThreads * 16;
 // launch keeps fewer for short rows).
 constexpr int kKeepChunks = 12;
 
+template <int KEEP>
+constexpr bool kBatchedMaxFirst = KEEP >= 6 && KEEP <= 8;
+
 template <typename T, int KEEP>
-__global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kBatchedMaxFirst<KEEP> ? 8 : 1))) void ce_rows_batched_kernel(
     const T* logits, T* grad, int64_t inner, int64_t valid_inner, int64_t os, int64_t is,
     int64_t gos, int64_t gis, int vocab, const int64_t* __restrict__ targets, int64_t tos,
     int64_t tis, int64_t ignore_index, int write_grad, CeWork* __restrict__ ws) {
@@ -549,13 +616,19 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
       row_ref(row, inner, valid_inner, os, is, targets, tos, tis, ignore_index, gos, gis);
   const T* p = logits + cur.off;
   T* g = grad + cur.goff;  // in the same 16-byte phase as p (checked on the host)
-  // head [0, head), body [head, head + nbody * V), tail [head + nbody * V, vocab)
-  const int lead = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T));
+  // head [0, head): the elements before the row's first 128-byte boundary; body [head,
+  // head + nbody * V); tail [head + nbody * V, vocab)
+  const int lead = static_cast<int>(((kLineBytes - (reinterpret_cast<uintptr_t>(p) & (kLineBytes - 1))) &
+                                     (kLineBytes - 1)) / sizeof(T));
   const int head = lead < vocab ? lead : vocab;
   const int nbody = (vocab - head) / V;
   const int tail_start = head + nbody * V;
   const int ntail = vocab - tail_start;
   const int body_bytes = nbody * 16;
+  // only kKeepChunks streams the body past its kept chunks (the launch gives the other
+  // instances rows that their kept chunks cover; without the streaming loops they need
+  // fewer registers)
+  const int stream_end = KEEP == kKeepChunks ? body_bytes : 0;
   const auto buf = row_buffer(const_cast<T*>(p) + head, body_bytes);
   const auto gbuf = row_buffer(g + head, body_bytes);
   const int voff = tid * 16;
@@ -587,35 +660,69 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     m = Elem<T>::to_f32(p[my_edge]);
     s = m == -INFINITY ? 0.0f : 1.0f;  // exp(x - x); a lone -inf contributes nothing
   }
-  float mk[KEEP];  // running max after kept chunk k: the reference of its exps
-#pragma unroll
-  for (int k = 0; k < KEEP; ++k) {
+  // the reference of kept chunk k's exps: the running max after it, or for 6 to 8 kept
+  // chunks (as in ce_rows_kernel, to stay under 64 VGPRs: 64 against 66-78 online) the
+  // thread's max over its edge element and all its kept chunks
+  constexpr bool kFirst = kBatchedMaxFirst<KEEP>;
+  float mk[kFirst ? 1 : KEEP];
+  const auto masked = [&](int k) -> Vec16<T> {
     Vec16<T> r = kv[k];
     if (voff + k * kChunkBytes >= body_bytes) {
       const uint32_t ninf = kNegInfWord<T>;
       r.raw = u32x4{ninf, ninf, ninf, ninf};
     }
-    float x[V];
+    return r;
+  };
+  if constexpr (kFirst) {
+    const float m0 = m;
 #pragma unroll
-    for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
-    float cm = x[0];
+    for (int k = 0; k < KEEP; ++k) {
+      const Vec16<T> r = masked(k);
 #pragma unroll
-    for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
-    const float nm = fmaxf(m, cm);
-    const float ref = nm == -INFINITY ? 0.0f : nm;
-    float add = 0.0f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float e = exp_shifted(x[i], ref);
-      add += e;
-      kv[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      for (int i = 0; i < V; ++i) m = fmaxf(m, Elem<T>::to_f32(r.e[i]));
     }
-    asm volatile("" : "+v"(kv[k].raw));  // packed here, not carried as fp32 across the barrier
-    s = s * exp_shifted(m, ref) + add;
-    m = nm;
-    mk[k] = nm;
+    const float ref = m == -INFINITY ? 0.0f : m;
+    s *= exp_shifted(m0, ref);
+#pragma unroll
+    for (int k = 0; k < KEEP; ++k) asm volatile("" : "+v"(kv[k].raw));  // convert again
+#pragma unroll
+    for (int k = 0; k < KEEP; ++k) {
+      const Vec16<T> r = masked(k);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float e = exp_shifted(Elem<T>::to_f32(r.e[i]), ref);
+        s += e;
+        kv[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      }
+      asm volatile("" : "+v"(kv[k].raw));
+    }
+    mk[0] = m;
+  } else {
+#pragma unroll
+    for (int k = 0; k < KEEP; ++k) {
+      const Vec16<T> r = masked(k);
+      float x[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) x[i] = Elem<T>::to_f32(r.e[i]);
+      float cm = x[0];
+#pragma unroll
+      for (int i = 1; i < V; ++i) cm = fmaxf(cm, x[i]);
+      const float nm = fmaxf(m, cm);
+      const float ref = nm == -INFINITY ? 0.0f : nm;
+      float add = 0.0f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float e = exp_shifted(x[i], ref);
+        add += e;
+        kv[k].e[i] = Elem<T>::from_f32(e * kExpScale<T>);
+      }
+      asm volatile("" : "+v"(kv[k].raw));  // packed here, not carried as fp32 across the barrier
+      s = s * exp_shifted(m, ref) + add;
+      m = nm;
+      mk[k] = nm;
+    }
   }
-  for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
+  for (int b = KEEP * kChunkBytes; b < stream_end; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
@@ -665,7 +772,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
 #pragma unroll
   for (int k = 0; k < KEEP; ++k) {
     // exp(m_k - M) / (S n) per chunk; 0 for a chunk whose reference is -inf
-    const float f = exp_shifted(mk[k], M) * (scale / kExpScale<T>);
+    const float f = exp_shifted(mk[kFirst ? 0 : k], M) * (scale / kExpScale<T>);
     Vec16<T> out;
 #pragma unroll
     for (int i = 0; i < V; ++i) out.e[i] = Elem<T>::from_f32(Elem<T>::to_f32(kv[k].e[i]) * f);
@@ -673,7 +780,7 @@ __global__ __launch_bounds__(kThreads) void ce_rows_batched_kernel(
     asm volatile("" : "+v"(vo));
     __builtin_amdgcn_raw_buffer_store_b128(out.raw, gbuf, vo, 0, kWriteThrough);
   }
-  for (int b = KEEP * kChunkBytes; b < body_bytes; b += kStreamBatchBytes) {
+  for (int b = KEEP * kChunkBytes; b < stream_end; b += kStreamBatchBytes) {
     Vec16<T> v[kStreamBatch];
 #pragma unroll
     for (int u = 0; u < kStreamBatch; ++u)
@@ -819,8 +926,10 @@ __global__ __launch_bounds__(kThreads) void ce_finish_kernel(CeWork* __restrict_
 // scalar is (torch's nll_loss backward leaves them 0).
 // The work items are (row, chunk of 1024 vectors or elements); a grid of up to 128 blocks
 // per CU walks them (a one-shot grid streams no faster and makes the common
-// grad_output == 1 launch several times dearer).  ALIGNED rows move 16-byte vectors (4 per
-// thread per chunk), nontemporal (touched once), otherwise single elements.
+// grad_output == 1 launch several times dearer).  The body moves in 16-byte vectors (4 per
+// thread per chunk, loads nontemporal: touched once); rows that do not start on a 128-byte
+// line (!ALIGNED) split off a head of elements up to the line and a tail of fewer than one
+// vector, one element per thread.
 constexpr int kScaleVecs = 4;
 
 template <typename T, bool ALIGNED>
@@ -865,11 +974,13 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* logits, const T* src, 
     if (!kDefer && skip) continue;
     T* p = logits + o * os + ii * is;
     const T* q = src + o * sos + ii * sis;  // same 16-byte phase as p (checked on the host)
-    // Unaligned rows: a head of elements before the first 16-byte boundary, a body of
-    // 16-byte vectors and a tail of fewer than V elements; aligned rows are all body.
+    // Rows not on 128-byte lines: a head of the elements before the first line (one per
+    // thread), a body of 16-byte vectors and a tail of fewer than V elements; rows on lines
+    // (ALIGNED) are all body.
     int lead = 0;
     if constexpr (!ALIGNED) {
-      lead = static_cast<int>(((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / sizeof(T));
+      lead = static_cast<int>(((kLineBytes - (reinterpret_cast<uintptr_t>(p) & (kLineBytes - 1))) &
+                               (kLineBytes - 1)) / sizeof(T));
       if (lead > vocab) lead = vocab;
     }
     const int nbody = (vocab - lead) / V;
@@ -986,49 +1097,50 @@ void launch_rows(const CeRows& d, int write_grad, CeWork* ws, int64_t rows, hipS
 }
 
 // Register-resident rows for up to 16 vectors per thread (131072 fp16/bf16 or 65536 fp32
-// elements) when every row is 16-byte aligned; other rows take the batched two-pass kernel
-// (the element-wise stream only for rows of 2 GB and more).
+// elements) when every row is 16-byte aligned and, up to 8 vectors per thread, starts on a
+// 128-byte line; other rows take the batched kernel (the element-wise stream only for rows
+// of 2 GB and more).
 template <typename T>
-void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, int64_t rows,
+void dispatch_rows(bool aligned, bool lines, const CeRows& d, int write_grad, CeWork* ws, int64_t rows,
                    hipStream_t st) {
   const int64_t per_thread = (static_cast<int64_t>(d.vocab) + int64_t{kThreads} * Elem<T>::VEC - 1) /
                              (int64_t{kThreads} * Elem<T>::VEC);
   const int64_t row_bytes = static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T));
-  if (aligned && write_grad != kGradWrite &&
-      row_bytes + int64_t{kLseThreads} * kLseBatch * 16 < (int64_t{1} << 31)) {
+  if (write_grad != kGradWrite && row_bytes + int64_t{kLseThreads} * kLseBatch * 16 < (int64_t{1} << 31)) {
     hipLaunchKernelGGL(ce_lse_kernel<T>, dim3(static_cast<unsigned>(rows)), dim3(kLseThreads), 0,
                        st, static_cast<const T*>(d.logits), d.inner, d.valid_inner, d.os, d.is,
                        d.vocab, d.targets, d.tos, d.tis, d.ignore_index, write_grad, ws);
     return;
   }
-  // fp16 never writes its gradient in the forward (it is deferred to the backward): its
-  // aligned rows take ce_lse_kernel above (or, from 2 GB, the stream kernel), so the
-  // register-resident kernel has no fp16 instances.
+  // fp16 never writes its gradient in the forward (it is deferred to the backward), and
+  // neither does a loss-only call: their rows take ce_lse_kernel above (from 2 GB, the
+  // stream kernel), so the register-resident and batched kernels have no fp16 instances.
   if constexpr (!std::is_same<T, _Float16>::value) {
-    if (aligned) {
+    // rows that do not start on a line take the batched kernel, which starts its vectors on
+    // one (up to 16 vectors per thread, the same single read of the row)
+    if (aligned && lines) {
 #define PT_CE_CASE(N)                                  \
   if (per_thread <= N) {                               \
     launch_rows<T, N>(d, write_grad, ws, rows, st);    \
     return;                                            \
   }
-    PT_CE_CASE(1)
-    PT_CE_CASE(2)
-    PT_CE_CASE(3)
-    PT_CE_CASE(4)
-    PT_CE_CASE(6)
-    PT_CE_CASE(8)
-    PT_CE_CASE(10)
-    PT_CE_CASE(12)
-    PT_CE_CASE(14)
-    PT_CE_CASE(16)
+      PT_CE_CASE(1)
+      PT_CE_CASE(2)
+      PT_CE_CASE(3)
+      PT_CE_CASE(4)
+      PT_CE_CASE(6)
+      PT_CE_CASE(7)
+      PT_CE_CASE(8)
+      PT_CE_CASE(10)
+      PT_CE_CASE(12)
+      PT_CE_CASE(14)
+      PT_CE_CASE(16)
 #undef PT_CE_CASE
     }
-  }
-  if (static_cast<int64_t>(d.vocab) * static_cast<int64_t>(sizeof(T)) + kStreamBatchBytes <
-      (int64_t{1} << 31)) {
-    // Rows whose body fits in 1, 2, 4 or 8 kept chunks are read once; longer rows keep
-    // kKeepChunks and stream the rest twice.  Fewer kept chunks leave room for two
-    // workgroups per CU.
+    if (row_bytes + kStreamBatchBytes < (int64_t{1} << 31)) {
+      // Rows whose body fits in 1, 2, 4, 6, 7, 8, 10, 12, 14 or 16 kept chunks are read
+      // once; longer rows keep kKeepChunks and stream the rest twice.  Up to 8 kept chunks
+      // leave room for two workgroups per CU.
 #define PT_CE_BATCHED(K)                                                                        \
   hipLaunchKernelGGL((ce_rows_batched_kernel<T, K>), dim3(static_cast<unsigned>(rows)),        \
                      dim3(kThreads),                                                           \
@@ -1036,19 +1148,34 @@ void dispatch_rows(bool aligned, const CeRows& d, int write_grad, CeWork* ws, in
                      static_cast<const T*>(d.logits), static_cast<T*>(d.grad), d.inner,          \
                      d.valid_inner, d.os, d.is, d.gos, d.gis, d.vocab, d.targets, d.tos, d.tis,  \
                      d.ignore_index, write_grad, ws)
-    if (per_thread <= 1) {
-      PT_CE_BATCHED(1);
-    } else if (per_thread <= 2) {
-      PT_CE_BATCHED(2);
-    } else if (per_thread <= 4) {
-      PT_CE_BATCHED(4);
-    } else if (per_thread <= 8) {
-      PT_CE_BATCHED(8);
-    } else {
-      PT_CE_BATCHED(kKeepChunks);
-    }
+      if (per_thread <= 1) {
+        PT_CE_BATCHED(1);
+      } else if (per_thread <= 2) {
+        PT_CE_BATCHED(2);
+      } else if (per_thread <= 4) {
+        PT_CE_BATCHED(4);
+      } else if (per_thread <= 6) {
+        PT_CE_BATCHED(6);
+      } else if (per_thread <= 7) {
+        PT_CE_BATCHED(7);
+      } else if (per_thread <= 8) {
+        PT_CE_BATCHED(8);
+      } else if (per_thread <= 10) {
+        PT_CE_BATCHED(10);
+      } else if (per_thread <= 12) {
+        PT_CE_BATCHED(12);
+      } else if (per_thread <= 14) {
+        PT_CE_BATCHED(14);
+      } else if (per_thread <= 16) {
+        PT_CE_BATCHED(16);
+      } else {
+        PT_CE_BATCHED(kKeepChunks);
+      }
 #undef PT_CE_BATCHED
-  } else if (aligned) {
+      return;
+    }
+  }
+  if (aligned) {
     hipLaunchKernelGGL((ce_rows_stream_kernel<T, true>), dim3(static_cast<unsigned>(rows)),
                        dim3(kThreads), 0, st, static_cast<const T*>(d.logits),
                        static_cast<T*>(d.grad), d.inner, d.valid_inner, d.os, d.is, d.gos, d.gis,
@@ -1103,13 +1230,17 @@ int ce_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, int64_
   const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
                        (outer <= 1 || (d.os * esize) % 16 == 0) &&
                        (inner <= 1 || (d.is * esize) % 16 == 0);
+  // every row starts on a 128-byte line
+  const bool lines = reinterpret_cast<uintptr_t>(d.logits) % kLineBytes == 0 &&
+                     (outer <= 1 || (d.os * esize) % kLineBytes == 0) &&
+                     (inner <= 1 || (d.is * esize) % kLineBytes == 0);
   const int mode = !write_grad ? kGradNone : (dtype == PT_FLOAT16 ? kGradDefer : kGradWrite);
   if (dtype == PT_FLOAT32) {
-    dispatch_rows<float>(aligned, d, mode, ws, rows, st);
+    dispatch_rows<float>(aligned, lines, d, mode, ws, rows, st);
   } else if (dtype == PT_FLOAT16) {
-    dispatch_rows<_Float16>(aligned, d, mode, ws, rows, st);
+    dispatch_rows<_Float16>(aligned, lines, d, mode, ws, rows, st);
   } else {
-    dispatch_rows<__bf16>(aligned, d, mode, ws, rows, st);
+    dispatch_rows<__bf16>(aligned, lines, d, mode, ws, rows, st);
   }
   if (int rc = check_launch(fn)) return rc;
   hipLaunchKernelGGL(ce_finish_kernel, dim3(1), dim3(kThreads), 0, st, ws, rows, loss_out);
@@ -1179,9 +1310,11 @@ int ce_scale_run(const char* fn, const CeRows& d, int64_t outer, int64_t inner, 
   const CeWork* ws = static_cast<const CeWork*>(workspace);
   hipStream_t st = as_stream(stream);
   const int esize = dtype_size(dtype);
-  const bool aligned = aligned16(d.logits) && (vocab * esize) % 16 == 0 &&
-                       (outer <= 1 || (d.os * esize) % 16 == 0) &&
-                       (inner <= 1 || (d.is * esize) % 16 == 0);
+  // all body: every row starts on a 128-byte line and holds whole 16-byte vectors
+  const bool aligned = reinterpret_cast<uintptr_t>(d.logits) % kLineBytes == 0 &&
+                       (vocab * esize) % 16 == 0 &&
+                       (outer <= 1 || (d.os * esize) % kLineBytes == 0) &&
+                       (inner <= 1 || (d.is * esize) % kLineBytes == 0);
   if (dtype == PT_FLOAT32) {
     scale_launch<float>(aligned, d, rows, grad_output, ws, st);
   } else if (dtype == PT_FLOAT16) {

@@ -68,13 +68,9 @@ def _fp16_grad_close(grad, ref_grad, scale, n_valid):
 
 def _loss_only_streams(logits, dtype) -> bool:
     """Whether the loss-only forward takes the read-only streaming kernel, while a forward
-    that writes the gradient takes another one: 16-byte-aligned rows."""
+    that writes the gradient takes another one: rows (aligned or not) below 2 GB."""
 
-    es = logits.element_size()
-    rows_aligned = all(
-        (st * es) % 16 == 0 for st, n in zip(logits.stride()[:-1], logits.shape[:-1]) if n > 1
-    )
-    return logits.data_ptr() % 16 == 0 and (logits.size(-1) * es) % 16 == 0 and rows_aligned
+    return logits.size(-1) * logits.element_size() + 256 * 8 * 16 < 2**31
 
 
 def _check(logits, targets, dtype):
@@ -311,7 +307,11 @@ def test_shifted_matches_the_train_loop_expression(gpu, dtype, b, s, v):
     assert abs(loss.item() - view_loss.item()) <= 1e-6 * abs(view_loss.item())
     buf = logits.clone()
     loss2, ws = ops.cross_entropy_shifted(buf, ids, write_grad=True)
-    assert loss2.item() == loss.item()
+    if dtype == torch.float16:
+        assert loss2.item() == loss.item()  # one read-only kernel (the gradient is deferred)
+    else:
+        # the kernel that writes the gradient against the read-only pass: another sum order
+        assert abs(loss2.item() - loss.item()) <= 1e-6 * abs(loss.item())
     assert ops.cross_entropy_status(ws) == 0
     if dtype == torch.float16:
         # the deferred gradient, written by the backward at a GradScaler-sized scale (odd
