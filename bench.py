@@ -1655,9 +1655,14 @@ DEMO_1M = dict(vocab=50257, hidden=20, intermediate=80, layers=8, heads=2, kv_he
 QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused",
                        "graph_fused_residual")
 # fp16 with a GradScaler reads the overflow flag on the host every step: eager only
-DEMO_VARIANTS = ("eager_reference", "eager_fused_modules", "eager_fused")
-STEP_VARIANTS = ("eager_reference", "eager_fused_modules", "eager_fused", "graph_reference", "graph_fused",
+DEMO_VARIANTS = ("eager_reference", "eager_notebook_flags", "eager_fused")
+STEP_VARIANTS = ("eager_reference", "eager_notebook_flags", "eager_fused", "graph_reference", "graph_fused",
                  "graph_fused_residual")
+# the modules' kernel flags a variant turns on (``model.triton_kernels``); the notebook's config
+# sets rmsnorm and swiglu and leaves rope, cross_entropy and adamw off
+_MODULE_FLAGS = frozenset({"rmsnorm", "swiglu", "rope"})
+_VARIANT_FLAGS = {"eager_reference": frozenset(), "graph_reference": frozenset(),
+                  "eager_notebook_flags": frozenset({"rmsnorm", "swiglu"})}
 
 
 class _StepBlock(torch.nn.Module):
@@ -1668,21 +1673,22 @@ class _StepBlock(torch.nn.Module):
     residual add, MLP norm, SwiGLU MLP, residual add.  The attention product runs in fp32 in
     every variant (plain PyTorch, identical between them)."""
 
-    def __init__(self, cfg: dict, fused: bool, use_rope: bool) -> None:
+    def __init__(self, cfg: dict, flags: frozenset, use_rope: bool) -> None:
         from picotron_amd.nn import RMSNorm, RotaryEmbedding, SwiGLU
 
         super().__init__()
         h, heads, kv = cfg["hidden"], cfg["heads"], cfg["kv_heads"]
         self.heads, self.kv_heads, self.head_dim, self.window = heads, kv, h // heads, cfg["window"]
-        self.attention_norm = RMSNorm(h, use_triton_rmsnorm=fused)
+        norm = "rmsnorm" in flags
+        self.attention_norm = RMSNorm(h, use_triton_rmsnorm=norm)
         self.query_projection = torch.nn.Linear(h, h, bias=False)
         self.key_projection = torch.nn.Linear(h, kv * self.head_dim, bias=False)
         self.value_projection = torch.nn.Linear(h, kv * self.head_dim, bias=False)
         self.output_projection = torch.nn.Linear(h, h, bias=False)
-        self.rotary_embedding = (RotaryEmbedding(self.head_dim, cfg["theta"], use_triton_rope=fused)
+        self.rotary_embedding = (RotaryEmbedding(self.head_dim, cfg["theta"], use_triton_rope="rope" in flags)
                                  if use_rope else None)
-        self.mlp_norm = RMSNorm(h, use_triton_rmsnorm=fused)
-        self.mlp = SwiGLU(h, cfg["intermediate"], use_triton_swiglu=fused)
+        self.mlp_norm = RMSNorm(h, use_triton_rmsnorm=norm)
+        self.mlp = SwiGLU(h, cfg["intermediate"], use_triton_swiglu="swiglu" in flags)
 
     def _attention(self, x: torch.Tensor) -> torch.Tensor:
         b, s, h = x.shape
@@ -1720,20 +1726,21 @@ class _StepBlock(torch.nn.Module):
 
 class _StepDecoder(torch.nn.Module):
     """The reference's decoder (src/picotron/models/picotron_decoder.py:133-220) with RoPE
-    positions, built from this package's modules; ``fused`` sets every module's kernel flag, as
-    ``model.triton_kernels`` does.  A tied output projection uses the token embeddings' weight
-    (`TiedOutputProjection`, picotron_decoder.py:49-67)."""
+    positions, built from this package's modules; ``flags`` names the modules whose kernel flag
+    is on ("rmsnorm", "swiglu", "rope"), as ``model.triton_kernels`` sets them.  A tied output
+    projection uses the token embeddings' weight (`TiedOutputProjection`,
+    picotron_decoder.py:49-67)."""
 
-    def __init__(self, cfg: dict, fused: bool, residual: bool = False) -> None:
+    def __init__(self, cfg: dict, flags: frozenset, residual: bool = False) -> None:
         from picotron_amd.nn import RMSNorm
 
         super().__init__()
         self.residual = residual
         v, h = cfg["vocab"], cfg["hidden"]
         self.token_embeddings = torch.nn.Embedding(v, h)
-        self.layers = torch.nn.ModuleList(_StepBlock(cfg, fused, i not in cfg["nope"])
+        self.layers = torch.nn.ModuleList(_StepBlock(cfg, flags, i not in cfg["nope"])
                                           for i in range(cfg["layers"]))
-        self.final_norm = RMSNorm(h, use_triton_rmsnorm=fused)
+        self.final_norm = RMSNorm(h, use_triton_rmsnorm="rmsnorm" in flags)
         self.output_projection = None if cfg["tied"] else torch.nn.Linear(h, v, bias=False)
 
     def _project(self, hidden: torch.Tensor) -> torch.Tensor:
@@ -1762,8 +1769,8 @@ class StepTrainer:
     backward, unscale_, clip, step, update; :155-160).
 
     ``variant``: ``eager_reference`` runs the modules with their kernel flags off, torch's loss
-    and torch's update (the reference's fallbacks); ``eager_fused_modules`` turns on the module
-    flags only (RMSNorm, SwiGLU and RoPE); ``eager_fused`` every flag, with
+    and torch's update (the reference's fallbacks); ``eager_notebook_flags`` turns on the flags
+    the notebook demo sets (RMSNorm and SwiGLU); ``eager_fused`` every flag (also RoPE), with
     ``CrossEntropyWithFallback(use_triton=True)`` and the fused update of
     ``AdamWStepWithFallback`` (``step(optimizer, max_grad_norm=)`` or ``step_with_grad_scaler``);
     the ``graph_*`` variants (bf16 configs) capture the whole step in one HIP graph
@@ -1781,11 +1788,11 @@ class StepTrainer:
         self.graphed = variant.startswith("graph")
         if self.graphed and cfg["dtype"] == "fp16":
             raise ValueError("the GradScaler step reads its overflow flag on the host: not capturable")
-        fused_modules = "fused" in variant
-        self.fused_update = fused_modules and not variant.endswith("modules")
+        flags = _VARIANT_FLAGS.get(variant, _MODULE_FLAGS)
+        self.fused_update = "fused" in variant
         self.autocast = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float16
         torch.manual_seed(seed)
-        self.model = _StepDecoder(cfg, fused_modules, residual=variant.endswith("residual")).cuda()
+        self.model = _StepDecoder(cfg, flags, residual=variant.endswith("residual")).cuda()
         self.optimizer = torch.optim.AdamW(self.model.parameters(), lr=cfg["lr"], betas=cfg["betas"],
                                            eps=1e-8, weight_decay=cfg["weight_decay"],
                                            capturable=self.graphed if capturable is None else capturable)

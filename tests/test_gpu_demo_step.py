@@ -1,8 +1,8 @@
 """The notebook demo's training step that bench.py times (examples/kaggle_demo_pretrain_sft_dpo.ipynb,
 cell 4: tied embeddings, grouped-query attention, a sliding window, one layer without RoPE, fp16
-with the train loop's GradScaler, clipping at 1.0): the step with the module flags on, and with
-every flag on (fused cross-entropy and the fused scaler + clip + AdamW update), follows the
-reference's fallbacks step for step."""
+with the train loop's GradScaler, clipping at 1.0): the step with the notebook's own flags
+(RMSNorm and SwiGLU), and with every flag on (also RoPE, the fused cross-entropy and the fused
+scaler + clip + AdamW update), follows the reference's fallbacks step for step."""
 
 from __future__ import annotations
 
@@ -14,7 +14,7 @@ from bench import DEMO_1M, StepTrainer
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("variant", ["eager_fused_modules", "eager_fused"])
+@pytest.mark.parametrize("variant", ["eager_notebook_flags", "eager_fused"])
 def test_demo_steps_follow_the_reference(gpu, variant):
     g = torch.Generator(device="cuda").manual_seed(23)
     batches = torch.randint(0, DEMO_1M["vocab"], (6, DEMO_1M["batch"], DEMO_1M["seq"]),
