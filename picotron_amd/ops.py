@@ -398,10 +398,12 @@ def ce_target_strides(targets: Tensor, outer: int, inner: int) -> tuple[int, int
 
 def ce_grad_buffer(logits: Tensor, class_dim: int = 1) -> Tensor | None:
     """An uninitialised tensor of the logits' shape and strides whose data starts in the same
-    16-byte phase as the logits', so that every gradient row starts in the phase of its logits
-    row, as the fused kernels require of a separate gradient (``class_dim``: the contiguous
-    class dimension, 1 for (N, C) and (N, C, d) inputs, 2 for the shifted (B, S, V) form).
-    None when the logits rows overlap in memory (an expanded tensor)."""
+    128-byte phase as the logits', so that every gradient row starts in the phase of its
+    logits row: the fused kernels require the same 16-byte phase of a separate gradient, and
+    split rows at the logits' 128-byte cache lines, which are then the gradient's lines too
+    (and the result bitwise the in-place call's).  ``class_dim``: the contiguous class
+    dimension, 1 for (N, C) and (N, C, d) inputs, 2 for the shifted (B, S, V) form.  None when
+    the logits rows overlap in memory (an expanded tensor)."""
 
     dims = list(zip(logits.shape, logits.stride()))
     rows = [d for i, d in enumerate(dims) if i != class_dim]
@@ -410,9 +412,9 @@ def ce_grad_buffer(logits: Tensor, class_dim: int = 1) -> Tensor | None:
     if logits.numel() == 0:
         return torch.empty_like(logits)
     span = 1 + sum((n - 1) * st for n, st in dims)
-    per16 = 16 // logits.element_size()
-    flat = torch.empty(span + per16, dtype=logits.dtype, device=logits.device)
-    offset = ((logits.data_ptr() - flat.data_ptr()) % 16) // logits.element_size()
+    per_line = 128 // logits.element_size()
+    flat = torch.empty(span + per_line, dtype=logits.dtype, device=logits.device)
+    offset = ((logits.data_ptr() - flat.data_ptr()) % 128) // logits.element_size()
     return flat.as_strided(logits.shape, logits.stride(), flat.storage_offset() + offset)
 
 

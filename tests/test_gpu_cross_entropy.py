@@ -80,7 +80,10 @@ def _check(logits, targets, dtype):
     assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
     buf = logits.clone()
     loss2, ws = ops.cross_entropy(buf, targets, write_grad=True)
-    if dtype == torch.float16 or not _loss_only_streams(logits, dtype):
+    # the kernels split rows at 128-byte lines, so a copy at another phase of a line sums
+    # in another order
+    same_split = (buf.data_ptr() - logits.data_ptr()) % 128 == 0
+    if (dtype == torch.float16 or not _loss_only_streams(logits, dtype)) and same_split:
         # the same kernel with and without the gradient (fp16 defers it to the backward)
         assert loss2.item() == loss.item()
     else:
@@ -179,28 +182,54 @@ def test_targets_at_the_ends_of_ragged_register_rows(gpu, dtype, vocab):
     _check(logits, targets, dtype)
 
 
+def _line_split_targets(logits, rows, vocab, es):
+    """Per row, a target on one side of the row's splits: its head (the elements before its
+    first 128-byte line), its body of 16-byte vectors from that line and its tail."""
+
+    v = 16 // es
+    picks = []
+    for r in range(rows):
+        addr = logits.data_ptr() + r * logits.stride(0) * es
+        head = min(((128 - addr % 128) % 128) // es, vocab)
+        tail_start = head + (vocab - head) // v * v
+        candidates = [c for c in (head - 1, head, tail_start - 1, tail_start, 0, vocab - 1) if 0 <= c < vocab]
+        picks.append(candidates[r % len(candidates)])
+    return picks
+
+
 @pytest.mark.parametrize(
     "dtype,vocab",
     [(torch.bfloat16, 50257), (torch.float16, 50257), (torch.float32, 1001), (torch.bfloat16, 151939),
-     (torch.float16, 200003)],
+     (torch.float16, 200003), (torch.bfloat16, 50256), (torch.float32, 32008), (torch.bfloat16, 128264)],
 )
 def test_targets_at_the_splits_of_unaligned_rows(gpu, dtype, vocab):
-    # Rows whose byte stride is not a multiple of 16 start at varying alignments; each is
-    # split into a head before its first 16-byte boundary, a body of 16-byte vectors and a
-    # tail.  Targets sit on both sides of each split and at the ends of the row.
+    # Rows whose byte stride is not a multiple of 128 start at varying places in a cache
+    # line; each is split into a head before its first 128-byte line, a body of 16-byte
+    # vectors and a tail.  Targets sit on both sides of each split and at the ends of the row.
     es = torch.tensor([], dtype=dtype).element_size()
-    v = 16 // es
     rows = 16
     logits = randn((rows, vocab), dtype, gpu, vocab + 13, 2.0)
-    picks = []
-    for r in range(rows):
-        addr = logits.data_ptr() + r * vocab * es
-        head = min(((16 - addr % 16) % 16) // es, vocab)
-        tail_start = head + (vocab - head) // v * v
-        candidates = [head - 1, head, tail_start - 1, tail_start, 0, vocab - 1]
-        picks.append([c for c in candidates if 0 <= c < vocab][r % 4])
+    picks = _line_split_targets(logits, rows, vocab, es)
     picks[5] = -100
     assert all(p == -100 or 0 <= p < vocab for p in picks)
+    _check(logits, torch.tensor(picks, device=gpu), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("vocab", [1, 7, 63, 65, 129, 1031, 9001])
+@pytest.mark.parametrize("offset", [0, 1, 3, 8, 17, 31, 32, 47, 63, 64, 71])
+def test_row_starts_in_every_line_phase(gpu, dtype, vocab, offset):
+    """Rows cut from one flat buffer at an element offset: with an odd vocabulary the rows
+    start at every phase of a 128-byte line, so heads run from none to a whole line (63
+    16-bit or 31 fp32 elements) and, for short rows, past the row's end; targets sit on
+    both sides of each split."""
+
+    es = torch.tensor([], dtype=dtype).element_size()
+    rows = 9
+    flat = randn((offset + rows * vocab,), dtype, gpu, 1000 * vocab + offset, 2.0)
+    logits = flat[offset:].view(rows, vocab)
+    picks = _line_split_targets(logits, rows, vocab, es)
+    picks[rows // 2] = -100
     _check(logits, torch.tensor(picks, device=gpu), dtype)
 
 
@@ -307,7 +336,7 @@ def test_shifted_matches_the_train_loop_expression(gpu, dtype, b, s, v):
     assert abs(loss.item() - view_loss.item()) <= 1e-6 * abs(view_loss.item())
     buf = logits.clone()
     loss2, ws = ops.cross_entropy_shifted(buf, ids, write_grad=True)
-    if dtype == torch.float16:
+    if dtype == torch.float16 and (buf.data_ptr() - logits.data_ptr()) % 128 == 0:
         assert loss2.item() == loss.item()  # one read-only kernel (the gradient is deferred)
     else:
         # the kernel that writes the gradient against the read-only pass: another sum order
@@ -580,7 +609,7 @@ def test_out_of_place_gradient_matches_in_place_bitwise(gpu, dtype, rows, vocab,
     n_valid = rows - 1
     ref_loss, ref_grad = o_ce.forward_backward(logits, targets)
     grad = ops.ce_grad_buffer(logits)
-    assert (grad.data_ptr() - logits.data_ptr()) % 16 == 0 and grad.stride() == logits.stride()
+    assert (grad.data_ptr() - logits.data_ptr()) % 128 == 0 and grad.stride() == logits.stride()
     loss, ws = ops.cross_entropy(logits, targets, write_grad=True, grad=grad)
     assert abs(loss.item() - ref_loss.item()) <= LOSS_RTOL * abs(ref_loss.item())
     assert ops.cross_entropy_status(ws) == 0
