@@ -163,8 +163,9 @@ int pt_rope(const void* x0, void* y0, const int64_t* desc0, const void* x1, void
  *   d loss / d logits = (softmax - onehot(target)) / n_valid   (0 for ignored rows)
  * is written in the same pass: with grad == NULL IN PLACE over the logits; otherwise into
  * the gradient rows grad + o*grad_outer_stride + i*grad_inner_stride (vocab contiguous),
- * each starting in the same 16-byte phase as its logits row (else PT_EINVAL), and the logits
- * are only read (one read of the logits and one write of the gradient either way).  fp16
+ * each starting in the same 16-byte phase as its logits row (else PT_EINVAL; the same
+ * 128-byte phase also keeps the gradient's stores on whole cache lines, as the kernels split
+ * rows at the logits' lines), and the logits are only read (one read of the logits and one write of the gradient either way).  fp16
  * logits are left unchanged and each row's log-sum-exp is kept in the workspace: the loss
  * scale of fp16 training arrives only with the backward, and softmax / n_valid is mostly
  * below fp16's smallest subnormal at language-model sizes, so pt_cross_entropy_scale_grad
