@@ -1654,7 +1654,8 @@ DEMO_1M = dict(vocab=50257, hidden=20, intermediate=80, layers=8, heads=2, kv_he
                theta=1e6, window=128, nope=(3,), tied=True)
 QUICKSTART_VARIANTS = ("eager_reference", "eager_fused", "graph_reference", "graph_fused",
                        "graph_fused_residual")
-# fp16 with a GradScaler reads the overflow flag on the host every step: eager only
+# fp16 with a GradScaler: eager only (torch's GradScaler.step reads the overflow flag on the
+# host every step; the captured fused fp16 step is switched off, see StepTrainer)
 DEMO_VARIANTS = ("eager_reference", "eager_notebook_flags", "eager_fused")
 STEP_VARIANTS = ("eager_reference", "eager_notebook_flags", "eager_fused", "graph_reference", "graph_fused",
                  "graph_fused_residual")
@@ -1786,10 +1787,14 @@ class StepTrainer:
             raise ValueError(f"unknown variant {variant}")
         self.cfg, self.variant = cfg, variant
         self.graphed = variant.startswith("graph")
-        if self.graphed and cfg["dtype"] == "fp16":
-            raise ValueError("the GradScaler step reads its overflow flag on the host: not capturable")
         flags = _VARIANT_FLAGS.get(variant, _MODULE_FLAGS)
         self.fused_update = "fused" in variant
+        if self.graphed and cfg["dtype"] == "fp16":
+            # torch's GradScaler.step reads its overflow flag on the host; the fused update
+            # decides on the device and captures (a whole captured update is tested), but the
+            # captured fp16 decoder step is switched off: its first run took a host
+            # segmentation fault in the autograd worker thread, whose cause is not found
+            raise ValueError("a captured fp16 step is switched off (see the comment above)")
         self.autocast = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float16
         torch.manual_seed(seed)
         self.model = _StepDecoder(cfg, flags, residual=variant.endswith("residual")).cuda()

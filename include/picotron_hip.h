@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define PT_ABI_VERSION 3
+#define PT_ABI_VERSION 4
 
 /* element type codes (storage types; arithmetic is always fp32) */
 #define PT_FLOAT32 0
@@ -293,6 +293,23 @@ int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t t
                               const int64_t* step_table, double lr, double beta1, double beta2,
                               double eps, double weight_decay, const float* grad_scale,
                               int write_grad, void* stream);
+
+/* pt_adamw_step_device_step with grad_scale, guarded by the overflow flag that pt_grad_stats
+ * left on the device (found_inf, int32): when it is 0 the launch is exactly
+ * pt_adamw_step_device_step; when it is set, parameters and moments are left untouched and
+ * every gradient is only multiplied by *inv_scale (device fp32), as
+ * torch.amp.GradScaler.unscale_ leaves the gradients of a skipped step.  The caller advances
+ * the device step counts by (1 - found_inf).  It replaces the host read in the train loop's
+ * fp16 update (src/picotron/training/train_loop.py:155-160: GradScaler.step reads found_inf
+ * on the host to skip optimizer.step()), so that the whole fp16 update -- statistics, this
+ * launch, the step counts and GradScaler.update -- runs without a host read and can be
+ * captured in a HIP graph.  Added in ABI version 4. */
+int pt_adamw_step_device_step_guarded(const int64_t* table, int64_t n_tensors,
+                                      int64_t total_blocks, const int64_t* step_table, double lr,
+                                      double beta1, double beta2, double eps,
+                                      double weight_decay, const float* grad_scale,
+                                      int write_grad, const int32_t* found_inf,
+                                      const float* inv_scale, void* stream);
 
 /* Mixed-precision / ZeRO gradient handling before the step
  * (src/picotron/parallel/zero.py:139-163 unscale_and_check_: a finite check of every

@@ -15,7 +15,7 @@ from pathlib import Path
 
 LIB_PATH = Path(os.environ.get("PICOTRON_HIP_LIB", Path(__file__).with_name("libpicotron_hip.so")))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 PT_FLOAT32 = 0
 PT_FLOAT16 = 1
@@ -114,6 +114,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_double, c_double, c_double, c_double, c_double,
          c_void_p, c_int, c_void_p],
+    ),
+    "pt_adamw_step_device_step_guarded": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_double, c_double, c_double, c_double, c_double,
+         c_void_p, c_int, c_void_p, c_void_p, c_void_p],
     ),
     "pt_grad_stats_workspace_bytes": (c_size_t, [c_int64]),
     "pt_grad_stats": (

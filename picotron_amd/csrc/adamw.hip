@@ -121,20 +121,31 @@ __device__ __forceinline__ void device_step_scalars(AdamScalars& s, const DevSte
 // SCALED: the gradient is multiplied by *grad_scale as it is read (torch's clipping
 // multiplies the stored gradient, g = g * coef, before the step reads it), and written back
 // when write_grad != 0.  DEVSTEP: bias corrections from the device step counts (DevStep).
+// `found` (may be null): the overflow flag of the gradient statistics, read on the device;
+// when it is set the step is skipped -- parameters and moments untouched -- and each
+// workgroup only unscales its block of the gradient by *inv_scale, as GradScaler.unscale_
+// leaves a skipped step's gradients (the caller advances no step count then).
 template <bool SCALED, bool DEVSTEP>
 __global__ __launch_bounds__(kThreads) void adamw_kernel(const AdamRec* __restrict__ table,
                                                          int64_t ntensors, AdamScalars s,
                                                          const float* __restrict__ grad_scale,
-                                                         int write_grad, DevStep ds) {
+                                                         int write_grad, DevStep ds,
+                                                         const int* __restrict__ found,
+                                                         const float* __restrict__ inv_scale) {
   const int64_t blk = blockIdx.x;
   const int64_t row = find_tensor(table, ntensors, blk);
   const AdamRec r = table[row];
-  if constexpr (DEVSTEP) device_step_scalars(s, ds, row);
-  const float gs = SCALED ? *grad_scale : 1.0f;
   const int64_t start = (blk - r.first_block) * kBlockElems;
   const int64_t end = (start + kBlockElems < r.n) ? start + kBlockElems : r.n;
-  const gptr<float> P = as_global<float>(r.p);
   const gptr<float> G = as_global<float>(r.g);
+  if (found != nullptr && *found != 0) {
+    const float is = *inv_scale;
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) G[i] = G[i] * is;
+    return;
+  }
+  if constexpr (DEVSTEP) device_step_scalars(s, ds, row);
+  const float gs = SCALED ? *grad_scale : 1.0f;
+  const gptr<float> P = as_global<float>(r.p);
   const gptr<float> M = as_global<float>(r.m);
   const gptr<float> Vv = as_global<float>(r.v);
   const bool vec_ok = ((r.p | r.g | r.m | r.v) & 15) == 0;
@@ -376,13 +387,14 @@ int step_occupancy() {
 
 template <bool SCALED, bool DEVSTEP>
 int launch_step(const int64_t* table, int64_t n_tensors, int64_t total_blocks, AdamScalars s,
-                const float* grad_scale, int write_grad, DevStep d, void* stream, const char* fn) {
+                const float* grad_scale, int write_grad, DevStep d, void* stream, const char* fn,
+                const int* found = nullptr, const float* inv_scale = nullptr) {
   const auto kernel = adamw_kernel<SCALED, DEVSTEP>;
   size_t lds = occupancy_lds(step_occupancy(), 0);
   if (allow_dynamic_lds(reinterpret_cast<const void*>(kernel), lds) != PT_OK) lds = 0;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(total_blocks)), dim3(kThreads), lds,
                      as_stream(stream), reinterpret_cast<const AdamRec*>(table), n_tensors, s,
-                     grad_scale, write_grad, d);
+                     grad_scale, write_grad, d, found, inv_scale);
   return check_launch(fn);
 }
 
@@ -471,6 +483,27 @@ int pt_adamw_step_device_step(const int64_t* table, int64_t n_tensors, int64_t t
                                    stream, "pt_adamw_step_device_step");
   return launch_step<false, true>(table, n_tensors, total_blocks, s, nullptr, 0, d, stream,
                                   "pt_adamw_step_device_step");
+}
+
+int pt_adamw_step_device_step_guarded(const int64_t* table, int64_t n_tensors,
+                                      int64_t total_blocks, const int64_t* step_table, double lr,
+                                      double beta1, double beta2, double eps,
+                                      double weight_decay, const float* grad_scale,
+                                      int write_grad, const int32_t* found_inf,
+                                      const float* inv_scale, void* stream) {
+  const char* fn = "pt_adamw_step_device_step_guarded";
+  const int rc = check_table(fn, table, n_tensors, total_blocks);
+  if (rc == -1) return ok();
+  if (rc != PT_OK) return rc;
+  if (!step_table || (reinterpret_cast<uintptr_t>(step_table) & 7u) != 0)
+    return fail(PT_EINVAL, std::string(fn) + ": null or misaligned step table");
+  if (!grad_scale || !found_inf || !inv_scale)
+    return fail(PT_EINVAL, std::string(fn) + ": null grad_scale, found_inf or inv_scale");
+  const AdamScalars s = host_scalars(lr, beta1, beta2, eps, weight_decay, 1.0);
+  const DevStep d{step_table, static_cast<float>(lr), static_cast<float>(beta1),
+                  static_cast<float>(beta2)};
+  return launch_step<true, true>(table, n_tensors, total_blocks, s, grad_scale, write_grad, d,
+                                 stream, fn, found_inf, inv_scale);
 }
 
 // One fp32 partial (and one int flag) per workgroup of the statistics walk, which has at

@@ -450,7 +450,8 @@ def triton_unscale_clip_and_step(
     return False
 
 
-def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float | None = None) -> bool:
+def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer,
+                            max_norm: float | None = None) -> bool | Tensor:
     """The train loop's single-GPU fp16 update, fused: ``grad_scaler.unscale_(optimizer)``,
     ``torch.nn.utils.clip_grad_norm_(params, max_norm)`` (when ``max_norm`` is given),
     ``grad_scaler.step(optimizer)`` and ``grad_scaler.update()`` (reference
@@ -469,6 +470,13 @@ def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float |
     them either way), and the scaler backs off exactly as torch's:
     the flag is recorded in the scaler's per-optimizer state as ``unscale_`` records it, and
     ``grad_scaler.update()`` consumes it.  Returns True when the step was skipped.
+
+    For an optimizer whose groups are all ``capturable=True`` and whose state exists (every
+    step after the first), nothing is read on the host: the AdamW launch reads the flag on
+    the device and either updates or only unscales, and the step counts advance by
+    ``1 - found_inf`` -- the same results, in a form a HIP graph can capture (warm up before
+    capturing; a step that would create state reads the flag as above).  The return value is
+    then the flag itself, a one-element int32 device tensor (nonzero when skipped).
 
     With a power-of-two scale (torch's defaults: 65536, growth 2, backoff 0.5) the unscaled
     gradients are bitwise torch's; the clip coefficient follows torch's formula with the norm
@@ -505,20 +513,35 @@ def triton_grad_scaler_step(grad_scaler, optimizer: Optimizer, max_norm: float |
 
 
 def _grad_scaler_step_committed(grad_scaler, state, optimizer, groups, device, scale, table,
-                                blocks, max_norm) -> bool:
+                                blocks, max_norm) -> bool | Tensor:
     from torch.amp.grad_scaler import OptState
 
     inv_scale = scale.double().reciprocal().float()
     _, multiplier, found_inf = ops.grad_stats(
         table, blocks, inv_scale, max_norm, ops.CLIP_CLAMP)
     launches, created = _prepare(optimizer, groups, device)
-    skipped = bool(found_inf.item())
-    if skipped:
-        for p in created:  # a skipped step leaves no state behind
-            del optimizer.state[p]
-        ops.grad_scale(table, blocks, inv_scale)
+    if launches and not created and all(steps is not None for _, _, steps, _ in launches):
+        # Every group capturable and its state in place: the overflow is decided on the
+        # device -- the guarded update skips itself and only unscales, the step counts
+        # advance by 1 - found_inf -- with no host read, so the update can be captured.
+        keep = (1.0 - found_inf.float()).reshape(())
+        steps_of = [optimizer.state[p]["step"] for _, params in groups for p in params]
+        # the list overload adds on the device (the 0-dim tensor overload reads the value
+        # on the host); step + 1.0 is the float32 addition of `step += 1`, step + 0.0 none
+        torch._foreach_add_(steps_of, [keep] * len(steps_of))
+        for launch_table, total_blocks, steps, hyper in launches:
+            ops.adamw_step_device_step(launch_table, total_blocks, steps, grad_scale=multiplier,
+                                       write_grad=True, found_inf=found_inf,
+                                       inv_scale=inv_scale.reshape(1), **hyper)
+        skipped = found_inf
     else:
-        _launch(optimizer, groups, launches, multiplier, True)
+        skipped = bool(found_inf.item())
+        if skipped:
+            for p in created:  # a skipped step leaves no state behind
+                del optimizer.state[p]
+            ops.grad_scale(table, blocks, inv_scale)
+        else:
+            _launch(optimizer, groups, launches, multiplier, True)
     state["found_inf_per_device"] = {device: found_inf.float()}
     state["stage"] = OptState.STEPPED
     grad_scaler.update()

@@ -702,23 +702,40 @@ def adamw_step_device_step(
     weight_decay: float,
     grad_scale: Tensor | None = None,
     write_grad: bool = False,
+    found_inf: Tensor | None = None,
+    inv_scale: Tensor | None = None,
 ) -> None:
     """:func:`adamw_step` (or :func:`adamw_step_scaled` with ``grad_scale``) for a capturable
     optimizer: the step counts are fp32 device scalars, already advanced, whose addresses
-    ``step_table_device`` lists in table row order."""
+    ``step_table_device`` lists in table row order.  With ``found_inf`` (the int32 flag of
+    :func:`grad_stats`; needs ``grad_scale`` and ``inv_scale``) the update runs only when the
+    flag is 0; when it is set the gradients are only multiplied by ``inv_scale``, decided on
+    the device (advance the step counts by ``1 - found_inf``)."""
 
     device = _check_cuda(table_device, step_table_device)
     if step_table_device.dtype != torch.int64 or step_table_device.numel() != table_device.size(0):
         raise ValueError("the step table needs one int64 address per table row")
-    if grad_scale is not None:
-        _check_cuda(grad_scale)
-        if grad_scale.dtype != torch.float32 or grad_scale.numel() != 1:
-            raise ValueError("grad_scale must be one fp32 element")
+    for name, t, dtype in (("grad_scale", grad_scale, torch.float32), ("inv_scale", inv_scale, torch.float32),
+                           ("found_inf", found_inf, torch.int32)):
+        if t is not None:
+            _check_cuda(t)
+            if t.dtype != dtype or t.numel() != 1:
+                raise ValueError(f"{name} must be one {dtype} element")
+    if found_inf is None:
+        _lib.call(
+            "pt_adamw_step_device_step",
+            table_device.data_ptr(), table_device.size(0), int(total_blocks), step_table_device.data_ptr(),
+            float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), _ptr(grad_scale),
+            int(write_grad), _stream(device),
+        )
+        return
+    if grad_scale is None or inv_scale is None:
+        raise ValueError("a guarded step needs grad_scale and inv_scale")
     _lib.call(
-        "pt_adamw_step_device_step",
+        "pt_adamw_step_device_step_guarded",
         table_device.data_ptr(), table_device.size(0), int(total_blocks), step_table_device.data_ptr(),
-        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), _ptr(grad_scale),
-        int(write_grad), _stream(device),
+        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay), grad_scale.data_ptr(),
+        int(write_grad), found_inf.data_ptr(), inv_scale.data_ptr(), _stream(device),
     )
 
 

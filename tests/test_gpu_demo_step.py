@@ -37,3 +37,30 @@ def test_demo_steps_follow_the_reference(gpu, variant):
         apart = float((p_o.detach() - p_r.detach()).abs().mean())
         assert moved > 0, name
         assert apart <= 0.05 * moved, f"{name}: mean |difference| {apart} against mean |update| {moved}"
+
+
+@pytest.mark.skip(reason="switched off: the first run took a host segmentation fault in the autograd "
+                         "worker thread (the eager step's backward right after the first replay; no GPU "
+                         "fault); its cause is not found, so the captured fp16 decoder step stays off. The "
+                         "captured fp16 update itself is tested in test_gpu_grad_scaler.py")
+def test_graph_replays_match_eager_steps(gpu):
+    """The fused fp16 step captured in one HIP graph (its GradScaler update decides each
+    step's overflow on the device) computes what the same steps compute eagerly with a
+    capturable optimizer."""
+
+    g = torch.Generator(device="cuda").manual_seed(29)
+    batches = torch.randint(0, DEMO_1M["vocab"], (6, DEMO_1M["batch"], DEMO_1M["seq"]),
+                            generator=g, device="cuda")
+    graphed = StepTrainer(DEMO_1M, "graph_fused")
+    eager = StepTrainer(DEMO_1M, "eager_fused", capturable=True)
+    graphed.prepare(batches[0])
+    eager.prepare(batches[0])
+    for i in range(1, 6):
+        loss_g = graphed.step(batches[i]).clone()
+        loss_e = eager.step(batches[i])
+        torch.cuda.synchronize()
+        print(f"captured demo step {i}: loss {float(loss_g):.6f} against {float(loss_e):.6f}", flush=True)
+        torch.testing.assert_close(loss_g, loss_e, rtol=1e-5, atol=1e-6, msg=f"step {i}")
+    assert graphed.scaler.get_scale() == eager.scaler.get_scale()
+    for (name, a), b in zip(graphed.model.named_parameters(), eager.model.parameters()):
+        torch.testing.assert_close(a.detach(), b.detach(), rtol=1e-5, atol=1e-6, msg=name)

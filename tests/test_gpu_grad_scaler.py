@@ -196,3 +196,103 @@ def test_a_failure_after_the_plain_step_began_is_not_retried(gpu, monkeypatch):
     sgd = torch.optim.SGD([fused[0]], lr=0.1)
     with pytest.warns(RuntimeWarning):
         AdamWStepWithFallback(use_triton=True).step(sgd)
+
+
+@pytest.mark.parametrize("max_norm", [None, 1e-3, 1e4])
+def test_capturable_optimizer_decides_the_overflow_on_the_device(gpu, max_norm):
+    """A capturable optimizer whose state exists takes the path that reads nothing on the
+    host: the guarded update skips itself on an overflow and only unscales, the step counts
+    advance by 1 - found_inf.  It follows torch's sequence step for step as the host-read
+    path does (a step that would create the state still reads the flag: the first one
+    overflows here and may leave no state behind, the second creates it)."""
+
+    fused, ref, _, opt_r, sc_f, sc_r = _setup(gpu, 15)
+    opt_f = torch.optim.AdamW(fused, capturable=True, **HP)
+    for step in range(8):
+        scale = sc_r.get_scale()
+        bad = OVERFLOWS.get(step)
+        print(f"capturable grad scaler step {step} scale {scale} bad {bad} max_norm {max_norm}", flush=True)
+        _set_grads(fused, ref, gpu, 100 * step, scale, bad)
+        _reference_step(sc_r, opt_r, ref, max_norm)
+        had_state = bool(opt_f.state)
+        skipped = triton_grad_scaler_step(sc_f, opt_f, max_norm)
+        if not had_state:
+            # the step that would create the state reads the flag on the host (step 0
+            # overflows and leaves none; step 1 creates it)
+            assert skipped is (bad is not None)
+            assert bool(opt_f.state) == (bad is None)
+        else:
+            assert isinstance(skipped, torch.Tensor) and bool(skipped.item()) == (bad is not None)
+        _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=bad is None or max_norm is None)
+    assert sc_f.get_scale() == 2.0 ** 15
+
+
+def test_captured_fp16_step_matches_eager_steps_through_overflows(gpu):
+    """A whole fp16 training step -- the scaled loss's backward, then the fused unscale +
+    clip + AdamW + scaler update -- captured in one HIP graph after warm-up and replayed over
+    inputs of which some overflow (inf, then NaN): every replay leaves the parameters,
+    moments, step counts, scale and growth tracker that the same steps leave when run
+    eagerly with the same capturable optimizer."""
+
+    sizes = [4097, 70_000]
+    n_steps, warmup = 10, 3
+    bad_steps = {4: float("inf"), 7: float("nan")}
+    inputs = []
+    for k in range(n_steps):
+        x = [randn((n,), torch.float32, gpu, 900 + 10 * k + i, 1e-3) for i, n in enumerate(sizes)]
+        if k in bad_steps:
+            x[1][123] = bad_steps[k]
+        inputs.append(x)
+
+    def build():
+        params = [torch.nn.Parameter(randn((n,), torch.float32, gpu, 40 + n, 0.02)) for n in sizes]
+        opt = torch.optim.AdamW(params, capturable=True, **HP)
+        sc = torch.amp.GradScaler("cuda", init_scale=2.0 ** 16, growth_interval=2)
+        return params, opt, sc, AdamWStepWithFallback(use_triton=True)
+
+    def step(run, x):
+        params, opt, sc, stepper = run
+        opt.zero_grad(set_to_none=False)
+        loss = sum((p * xi).sum() for p, xi in zip(params, x))
+        sc.scale(loss).backward()
+        stepper.step_with_grad_scaler(sc, opt, 1.0)
+
+    def state_of(run):
+        params, opt, sc, _ = run
+        out = [sc.get_scale(), int(sc._growth_tracker.item())]
+        for p in params:
+            st = opt.state[p]
+            out.append((p.detach().clone(), st["exp_avg"].clone(), st["exp_avg_sq"].clone(), float(st["step"])))
+        return out
+
+    eager, graphed = build(), build()
+    static_x = [t.clone() for t in inputs[0]]
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # no fallback
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for k in range(warmup):
+                for s, t in zip(static_x, inputs[k]):
+                    s.copy_(t)
+                step(graphed, static_x)
+        torch.cuda.current_stream().wait_stream(side)
+        for k in range(warmup):
+            step(eager, inputs[k])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(graphed, static_x)
+        for k in range(warmup, n_steps):
+            for s, t in zip(static_x, inputs[k]):
+                s.copy_(t)
+            graph.replay()
+            step(eager, inputs[k])
+            torch.cuda.synchronize()
+            print(f"captured fp16 step {k} (bad {bad_steps.get(k)})", flush=True)
+            a, b = state_of(graphed), state_of(eager)
+            assert a[:2] == b[:2], f"step {k}: scale / growth tracker {a[:2]} against {b[:2]}"
+            for (pa, ma, va, sa), (pb, mb, vb, sb) in zip(a[2:], b[2:]):
+                assert sa == sb, f"step {k}: step count {sa} against {sb}"
+                assert torch.equal(pa, pb) and torch.equal(ma, mb) and torch.equal(va, vb), f"step {k}"
+    # two overflow steps were skipped: 10 steps, 8 applied
+    assert state_of(eager)[2][3] == n_steps - len(bad_steps)
