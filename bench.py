@@ -514,7 +514,7 @@ class HeadlineWorkload(Workload):
         # for a while, which slows the host-bound eager steps; a failure here (it runs torch's
         # own kernels and graph capture too) is reported in the line rather than ending it
         steps_out = {}
-        for key, describe, count in (("quickstart_step", _quickstart_line, 200), ("demo_step", _demo_line, 50)):
+        for key, describe, count in (("quickstart_step", _quickstart_line, 200), ("demo_step", _demo_line, 20)):
             try:
                 steps_out[key] = describe(steps=count)
             except Exception as error:  # noqa: BLE001
