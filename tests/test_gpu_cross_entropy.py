@@ -269,6 +269,45 @@ def test_train_loop_view(gpu):
     assert torch.equal(full[:, -1, :], last)  # the unused last position is untouched
 
 
+# Two and more rows per CU (256 CUs here) of 9 to 16 vectors per thread on 128-byte lines
+# (vocabularies below: multiples of 64 bf16 or 32 fp32 logits): the register rows of one
+# workgroup per CU, several after one another on each CU
+MANY_ROWS = 2 * 256 + 9
+
+
+@pytest.mark.parametrize(
+    "dtype,vocab",
+    [(torch.bfloat16, 73_024), (torch.bfloat16, 90_112), (torch.bfloat16, 110_592), (torch.bfloat16, 128_256),
+     (torch.bfloat16, 131_072), (torch.float32, 40_000), (torch.float32, 51_200), (torch.float32, 65_536)],
+)
+def test_many_long_rows(gpu, dtype, vocab):
+    """Every row against the oracle, with ignored rows (zeros stored) in runs and alone, the
+    last rows of the grid, and targets at the first and last logit and at the ends of the
+    last chunk."""
+
+    v = 16 // torch.tensor([], dtype=dtype).element_size()
+    per_thread = -(-vocab // (1024 * v))
+    last_chunk = (per_thread - 1) * 1024 * v
+    logits = randn((MANY_ROWS, vocab), dtype, gpu, vocab + 31, 2.0)
+    g = torch.Generator(device=gpu).manual_seed(vocab)
+    targets = torch.randint(0, vocab, (MANY_ROWS,), generator=g, device=gpu)
+    picks = [0, vocab - 1, last_chunk, max(last_chunk - v, 0), min(last_chunk + v - 1, vocab - 1)]
+    for i, p in enumerate(picks):
+        targets[i * 97 % MANY_ROWS] = p
+    targets[3] = targets[255] = targets[256] = targets[257] = -100  # one row of each CU's second turn
+    targets[-1] = targets[-2] = -100
+    _check(logits, targets, dtype)
+
+
+def test_many_long_rows_flag_a_bad_target(gpu):
+    logits = randn((MANY_ROWS, 128_256), torch.bfloat16, gpu, 77, 2.0)
+    targets = torch.zeros(MANY_ROWS, dtype=torch.int64, device=gpu)
+    targets[300] = 128_256
+    buf = logits.clone()
+    loss, ws = ops.cross_entropy(buf, targets, write_grad=True)
+    assert math.isnan(loss.item()) and ops.cross_entropy_status(ws) & 1
+
+
 def test_ignored_rows_and_bad_targets(gpu):
     logits = randn((6, 100), torch.float32, gpu, 71)
     targets = torch.full((6,), -100, device=gpu)
