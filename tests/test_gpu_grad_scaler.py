@@ -296,3 +296,34 @@ def test_captured_fp16_step_matches_eager_steps_through_overflows(gpu):
                 assert torch.equal(pa, pb) and torch.equal(ma, mb) and torch.equal(va, vb), f"step {k}"
     # two overflow steps were skipped: 10 steps, 8 applied
     assert state_of(eager)[2][3] == n_steps - len(bad_steps)
+
+
+@pytest.mark.parametrize("both_capturable", [True, False])
+def test_groups_decide_on_the_device_only_when_all_are_capturable(gpu, both_capturable):
+    """Two parameter groups with their own learning rate and weight decay: with both
+    capturable the overflow is decided on the device (a device flag is returned), with one
+    not the host reads it; either way the steps follow torch's sequence through overflows."""
+
+    fused, ref, _, _, sc_f, sc_r = _setup(gpu, 25)
+    split = 4
+
+    def groups(params, capturable):
+        return [dict(params=params[:split], lr=3e-4, weight_decay=0.1, capturable=capturable[0]),
+                dict(params=params[split:], lr=1e-3, weight_decay=0.0, capturable=capturable[1])]
+
+    caps = (True, both_capturable)
+    opt_f = torch.optim.AdamW(groups(fused, caps), betas=(0.9, 0.95), eps=1e-8)
+    opt_r = torch.optim.AdamW(groups(ref, (False, False)), betas=(0.9, 0.95), eps=1e-8, foreach=False)
+    for step in range(6):
+        scale = sc_r.get_scale()
+        bad = {2: float("inf"), 4: float("nan")}.get(step)
+        print(f"groups step {step} scale {scale} bad {bad} capturable {caps}", flush=True)
+        _set_grads(fused, ref, gpu, 700 + 100 * step, scale, bad)
+        _reference_step(sc_r, opt_r, ref, 1.0)
+        had_state = bool(opt_f.state)
+        skipped = triton_grad_scaler_step(sc_f, opt_f, 1.0)
+        if had_state and both_capturable:
+            assert isinstance(skipped, torch.Tensor) and bool(skipped.item()) == (bad is not None)
+        else:
+            assert skipped is (bad is not None)
+        _compare(fused, ref, opt_f, opt_r, sc_f, sc_r, grads_too=bad is None)
