@@ -575,9 +575,10 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
   }
 }
 
-// Rows that the register-resident kernel does not take -- longer than it holds, or, up to
-// 8 vectors per thread, not starting on a 128-byte cache line -- with row_bytes +
-// kStreamBatchBytes < 2^31: one 1024-thread workgroup per row in two passes.  A row is split
+// Rows that the register-resident kernel does not take -- longer than it holds, or not
+// starting on a 128-byte cache line -- with row_bytes + kStreamBatchBytes < 2^31: one
+// 1024-thread workgroup per row; rows of up to 16 vectors per thread are held whole in
+// registers and read once, longer ones in two passes.  A row is split
 // into a head of the elements before its first 128-byte boundary (at most 127 bytes' worth,
 // one per thread, from thread 0), a body of 16-byte vectors read in batches of kStreamBatch
 // per thread with raw buffer loads (the hardware range check drops the ragged end), and a
@@ -585,15 +586,17 @@ __global__ __launch_bounds__(kLseThreads) void ce_lse_kernel(
 // line makes each wave's 1024-byte access cover 8 whole lines rather than 9 partial ones: a
 // [8160, V] bf16 forward streams at 5.8-6.0 TB/s for V a multiple of 64 and 4.7-4.9 TB/s for
 // other multiples of 8 when the body starts at the row (50000, 50256, 54000, 57000, 62000).
+// The kept chunks are reduced and written as in ce_rows_kernel; the part of a longer row
+// past them takes two passes:
 //   1. cached loads (the row stays in the Infinity Cache for pass 2) and an online max /
-//      sum per thread, reduced as in ce_rows_kernel (one barrier);
-//   2. the row re-read (nontemporal: last use), exp(x - M) / (S * n_valid) written over it;
+//      sum per thread, reduced with the kept chunks' (one barrier);
+//   2. the part re-read (nontemporal: last use), exp(x - M) / (S * n_valid) written over it;
 //      the thread that wrote the target's element then stores (softmax_t - 1) / n_valid.
 constexpr int kStreamBatch = 4;
 constexpr int kStreamBatchBytes = kStreamBatch * kThreads * 16;
-// Leading body chunks (1024 vectors each) held in registers as exps between the passes, as
-// in ce_rows_kernel: only the body beyond them is read twice (at most kKeepChunks; the
-// launch keeps fewer for short rows).
+// Leading body chunks (1024 vectors each) held in registers as exps, as in ce_rows_kernel:
+// the launch keeps as many as a row needs up to 16, and kKeepChunks of a longer row, whose
+// body beyond them is read twice.
 constexpr int kKeepChunks = 12;
 
 template <int KEEP>
