@@ -53,6 +53,40 @@ def test_rmsnorm(gpu, dtype, cols, bad, where):
     torch.testing.assert_close(dw[fin], dw_r[fin], rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("bad", BAD)
+@pytest.mark.parametrize("where", ["x", "residual", "dy", "dh_in"])
+def test_residual_rmsnorm(gpu, dtype, bad, where):
+    """The residual add fused into the norm: h = x + residual carries a bad value into the
+    norm, dh_in adds after it; the reference is the add, then the norm's PyTorch path, with
+    dh_in added to its input gradient."""
+
+    cols = 4096
+    x = randn((6, cols), dtype, gpu, 11, 1.0)
+    res = randn((6, cols), dtype, gpu, 12, 1.0)
+    w = randn((cols,), torch.float32, gpu, 13, 0.1, 1.0)
+    dy = randn((6, cols), dtype, gpu, 14, 1.0)
+    dh_in = randn((6, cols), dtype, gpu, 15, 1.0)
+    {"x": x, "residual": res, "dy": dy, "dh_in": dh_in}[where][1, 7] = bad
+    h, y, rstd = ops.residual_rmsnorm_fwd(x, res, w, 1e-5)
+    dh, dw = ops.residual_rmsnorm_bwd(dy, dh_in, h, w, rstd)
+    h_r = (x.float() + res.float()).to(dtype)
+    y_r, rstd_r, dx_r, dw_r = o_rms.fallback_forward_backward(h_r, w, 1e-5, dy)
+    dh_r = (dx_r.float() + dh_in.float()).to(dtype)
+    _same(h, h_r, dtype, "h")
+    _same(y, y_r, dtype, "y")
+    _same(rstd, rstd_r, torch.float32, "rstd")
+    # the kernel adds dh_in before its single rounding; the reference rounds twice
+    fin = torch.isfinite(dh_r.float())
+    assert torch.equal(torch.isfinite(dh.float()), fin)
+    torch.testing.assert_close(dh.float()[fin], dh_r.float()[fin], rtol=2 * TOL[dtype]["rtol"],
+                               atol=2 * TOL[dtype]["atol"])
+    assert bool(torch.isfinite(dh[[0, 2, 3, 4, 5]].float()).all())
+    fin = torch.isfinite(dw_r)
+    assert torch.equal(torch.isfinite(dw), fin)
+    torch.testing.assert_close(dw[fin], dw_r[fin], rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("bad", BAD)
 @pytest.mark.parametrize("where", ["gate", "up", "dy"])
