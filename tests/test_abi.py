@@ -70,6 +70,10 @@ def test_workspace_queries():
         ("pt_adamw_step", (None, 1, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
         ("pt_adamw_step_device_step", (None, 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
         ("pt_adamw_step_device_step", (ctypes.addressof(_HOST_TABLE), 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None), _lib.PT_EINVAL),
+        # the guarded step: a step table, and grad_scale, found_inf and inv_scale, are required
+        ("pt_adamw_step_device_step_guarded", (ctypes.addressof(_HOST_TABLE), 1, 1, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, 16, 1, 16, 16, None), _lib.PT_EINVAL),
+        ("pt_adamw_step_device_step_guarded", (ctypes.addressof(_HOST_TABLE), 1, 1, ctypes.addressof(_HOST_TABLE), 1e-3, 0.9, 0.99, 1e-8, 0.0, 16, 1, None, 16, None), _lib.PT_EINVAL),
+        ("pt_adamw_step_device_step_guarded", (ctypes.addressof(_HOST_TABLE), 1, 1, ctypes.addressof(_HOST_TABLE), 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 1, 16, 16, None), _lib.PT_EINVAL),
         # more records than blocks: a record without a block (an empty tensor) is refused
         ("pt_adamw_step", (ctypes.addressof(_HOST_TABLE), 2, 1, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None), _lib.PT_EINVAL),
         ("pt_grad_scale", (ctypes.addressof(_HOST_TABLE), 3, 2, None, None), _lib.PT_EINVAL),
@@ -102,6 +106,7 @@ def test_empty_inputs_are_no_ops():
     assert lib.pt_swiglu_bwd(None, None, None, None, None, 5, 2, None) == _lib.PT_OK
     assert lib.pt_adamw_step(None, 0, 0, 1e-3, 0.9, 0.99, 1e-8, 0.0, 1.0, None) == _lib.PT_OK
     assert lib.pt_adamw_step_device_step(None, 0, 0, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 0, None) == _lib.PT_OK
+    assert lib.pt_adamw_step_device_step_guarded(None, 0, 0, None, 1e-3, 0.9, 0.99, 1e-8, 0.0, None, 1, None, None, None) == _lib.PT_OK
     assert lib.pt_cross_entropy_shifted_scale_grad(None, 0, 5, 0, 8, 8, None, 5, 1, -100, None, None, 0, 0, None, 2, None) == _lib.PT_OK
     assert lib.pt_last_error() == b""
 
