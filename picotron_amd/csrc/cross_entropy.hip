@@ -1019,6 +1019,21 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* logits, const T* src, 
     const int64_t trel64 = tgt - lead - static_cast<int64_t>(cstart) * V;
     const int trel = (trel64 >= 0 && trel64 < int64_t{256} * kScaleVecs * V) ? static_cast<int>(trel64) : -1;
     const int tid = static_cast<int>(threadIdx.x);
+    // In a row not on a line, the first item also takes the head elements and the item of
+    // the body's last chunk the tail elements (one per thread), so that each end of the row
+    // is written by one item; their loads go out with the vector loads, so that their
+    // latency overlaps them rather than following the vector stores.
+    T head_v{}, tail_v{};
+    bool has_head = false, has_tail = false;
+    const int tail_j = lead + nbody * V + tid;
+    if constexpr (!ALIGNED) {
+      const int last_c = nbody > 0 ? (nbody - 1) / (256 * kScaleVecs) : 0;
+      const bool read = !(kDefer && skip);  // an ignored fp16 row is written as zeros
+      has_head = c == 0 && tid < lead;
+      has_tail = c == last_c && tid < V && tail_j < vocab;
+      if (has_head && read) head_v = q[tid];
+      if (has_tail && read) tail_v = q[tail_j];
+    }
     Vec16<T> in[kScaleVecs];
 #pragma unroll
     for (int k = 0; k < kScaleVecs; ++k)
@@ -1046,19 +1061,15 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(T* logits, const T* src, 
     for (int k = 0; k < kScaleVecs; ++k)
       __builtin_amdgcn_raw_buffer_store_b128(out[k].raw, sbuf, (k * 256 + tid) * 16, 0, kWriteThrough);
     if constexpr (!ALIGNED) {
-      if (c == 0) {
-        // The value is rounded to fp32 before the conversion, as in the vector path (left
-        // alone, the compiler fuses the last multiply and the fp16 conversion into one rounding).
-        const auto fix = [&](T v, int64_t j) {
-          float y = skip ? 0.0f : grad(Elem<T>::to_f32(v), j);
-          asm volatile("" : "+v"(y));
-          return Elem<T>::from_f32(y);
-        };
-        const int t = static_cast<int>(threadIdx.x);
-        if (t < lead) p[t] = fix(q[t], t);
-        const int tail = lead + nbody * V + t;
-        if (t < V && tail < vocab) p[tail] = fix(q[tail], tail);
-      }
+      // The value is rounded to fp32 before the conversion, as in the vector path (left
+      // alone, the compiler fuses the last multiply and the fp16 conversion into one rounding).
+      const auto fix = [&](T v, int64_t j) {
+        float y = skip ? 0.0f : grad(Elem<T>::to_f32(v), j);
+        asm volatile("" : "+v"(y));
+        return Elem<T>::from_f32(y);
+      };
+      if (has_head) p[tid] = fix(head_v, tid);
+      if (has_tail) p[tail_j] = fix(tail_v, tail_j);
     }
   }
 }
