@@ -1,6 +1,6 @@
 """Benchmark of the fused memory-bound kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|ce_train_fp16|ce_demo_fp16|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|rmsnorm|residual_rmsnorm|swiglu|rope|ce|ce_train|ce_train_fp16|ce_demo_fp16|ce_vocabs|adamw|adamw_list|adamw_clip|zero_step|fp16_step|modules|copy]
 
 Default workload (the headline metric, "RMSNorm/SwiGLU fwd+bwd"): ``--layers`` decoder layers
 (default 4), each with its own activations: the RMSNorm forward of a bf16 [16384 tokens
@@ -2081,6 +2081,93 @@ def _cpu_line(wl: Workload) -> dict | None:
     return cpu
 
 
+# ------------------------------------------------------------------ cross-entropy by vocabulary
+
+# Vocabularies that start rows on 128-byte lines (multiples of 64 16-bit logits) and ones that
+# do not: odd (GPT-2's 50257), multiples of 8 and 16 (rows on 16-byte boundaries), and the
+# common model vocabularies around them.
+CE_VOCABS = (32000, 32001, 32008, 48000, 50256, 50257, 50304, 57000, 64000, 128256, 128264, 151936)
+
+
+def ce_vocab_figures(rows: int = 8160, vocabs=CE_VOCABS, steps: int = 20) -> dict:
+    """Per vocabulary, [rows, V] logits: the bf16 forward writing the gradient in place and
+    the fp16 forward (log-sum-exps only) and backward (the gradient at a GradScaler-sized
+    scale, in place), each timed with HIP events over ``steps`` calls after 3 warm-up calls;
+    GB/s on the algorithmic bytes (bf16: read + write; fp16: read, then read + write)."""
+
+    from picotron_amd import ops
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+
+    def timed(fn) -> float:
+        for _ in range(3):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps * 1e3
+
+    out = {}
+    for v in vocabs:
+        targets = torch.randint(0, v, (rows,), device="cuda", generator=g)
+        row = {"line_aligned": (v * 2) % 128 == 0}
+        buf = (torch.randn(rows, v, device="cuda", generator=g) * 2).to(torch.bfloat16)
+        us = timed(lambda: ops.cross_entropy(buf, targets, write_grad=True))
+        row["bf16_forward_us"] = round(us, 1)
+        row["bf16_forward_gbs"] = round(2 * rows * v * 2 / us / 1e3, 1)
+        del buf
+        buf = (torch.randn(rows, v, device="cuda", generator=g) * 2).to(torch.float16)
+        state = {}
+
+        def forward():
+            state["ws"] = ops.cross_entropy(buf, targets, write_grad=True)[1]
+
+        us = timed(forward)
+        row["fp16_forward_us"] = round(us, 1)
+        row["fp16_forward_gbs"] = round(rows * v * 2 / us / 1e3, 1)
+        scale = torch.full((), 65536.0, device="cuda")
+        us = timed(lambda: ops.cross_entropy_scale_grad(buf, targets, scale, workspace=state["ws"]))
+        row["fp16_backward_us"] = round(us, 1)
+        row["fp16_backward_gbs"] = round(2 * rows * v * 2 / us / 1e3, 1)
+        del buf, state
+        torch.cuda.empty_cache()
+        out[str(v)] = row
+    return out
+
+
+def _ce_vocabs_main(args) -> int:
+    """The cross-entropy kernels across vocabularies as one line: value = the lowest bf16
+    forward GB/s of the list (the figure row alignment moves most)."""
+
+    rows = 8160
+    figs = ce_vocab_figures(rows, CE_VOCABS, args.steps)
+    worst = min(f["bf16_forward_gbs"] for f in figs.values())
+    result = {
+        "metric": "cross-entropy GB/s by vocabulary, [8160, V] (lowest bf16 forward of the list)",
+        "value": worst,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": 3,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16/f16",
+        "data": "synthetic (seeded on device)",
+        "config": {"workload": f"{rows} rows x V logits, in place; HIP events per call", "parallelism": "single GPU",
+                   "vocabularies": figs},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def _step_main(args) -> int:
     """A whole training step as its own line: value = tokens per second of the lead variant
     (the graph-captured fused step for the quickstart model, the fused eager step for the
@@ -2127,7 +2214,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted([*WORKLOADS, "quickstart_step", "demo_step"]),
+    parser.add_argument("--workload", choices=sorted([*WORKLOADS, "quickstart_step", "demo_step", "ce_vocabs"]),
                         default="headline")
     parser.add_argument("--variant", choices=("all", *STEP_VARIANTS), default="all",
                         help="quickstart_step and demo_step only: the step variant(s) to time")
@@ -2157,6 +2244,8 @@ def main() -> int:
 
     if args.workload in ("quickstart_step", "demo_step"):
         return _step_main(args)
+    if args.workload == "ce_vocabs":
+        return _ce_vocabs_main(args)
     global _WITH_CPU_BASELINE
     _WITH_CPU_BASELINE = not args.no_cpu_baseline
     layers = args.layers or DEFAULT_LAYERS[args.workload]
